@@ -1,0 +1,181 @@
+"""GPU parity of the Muon kernels (gfx950) through the C ABI.
+
+Building blocks (Gram, polynomial, update GEMMs) against float64 products of
+the same bf16 inputs: every output within one bf16 rounding of the exact
+value.  The full Muon step against the CPU oracle (oracle/muon.py): momentum
+bit-exact, the orthogonalised update within bf16 noise (relative Frobenius
+error <= 1e-2; two correct bf16 implementations differ by 0.3-0.6%), and the
+parameters within the reference tolerance (atol = rtol = 1e-2,
+muon_benchmark.py:105) and far tighter.  Batched launches must equal
+single-matrix launches bit for bit.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from helpers import muon_inputs, rel_fro
+from triton_muon_adamw.muon import HipMuon, muon_step, newton_shultz_step
+from triton_muon_adamw.muon import solve_ns_kernel_1, solve_ns_kernel_2, solve_ns_kernel_3
+from triton_muon_adamw.muon.hip_muon import scaled_lr
+
+pytestmark = pytest.mark.gpu
+
+COEFFS = (3.4445, -4.7750, 2.0315)
+
+
+def _bf16_close(got: torch.Tensor, exact: np.ndarray, rel_floor: float = 1e-5):
+    """|got - exact| <= one bf16 ulp of exact (+ a floor for cancellation)."""
+    g = got.float().cpu().numpy().astype(np.float64)
+    e = np.asarray(exact, dtype=np.float64)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(e), 1e-30))) - 7)
+    bad = np.abs(g - e) > ulp + rel_floor * np.abs(e).max()
+    assert not bad.any(), f"{bad.sum()} elements off by more than 1 bf16 ulp (max err {np.abs(g - e).max()})"
+
+
+def _rand_bf16(shape, seed, std=1.0):
+    gen = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=gen) * std).bfloat16()
+
+
+@pytest.mark.parametrize("m,k", [(128, 64), (256, 640), (200, 333), (2048, 1024)])
+def test_gram_exact_symmetric(gpu, m, k):
+    X = _rand_bf16((m, k), 11, std=k**-0.5)
+    A = torch.empty((m, m), dtype=torch.bfloat16, device=gpu)
+    solve_ns_kernel_1(X.to(gpu), A)
+    torch.cuda.synchronize()
+    assert torch.equal(A, A.T), "Gram output must be exactly symmetric"
+    Xd = X.double().numpy()
+    _bf16_close(A, Xd @ Xd.T)
+
+
+@pytest.mark.parametrize("m", [128, 384, 2048])
+def test_poly_exact_symmetric(gpu, m):
+    X = _rand_bf16((m, 2 * m), 12, std=(2 * m) ** -0.5)
+    A = torch.empty((m, m), dtype=torch.bfloat16, device=gpu)
+    solve_ns_kernel_1(X.to(gpu), A)
+    B = torch.empty_like(A)
+    b, c = COEFFS[1], COEFFS[2]
+    solve_ns_kernel_2(A, b, c, B)
+    torch.cuda.synchronize()
+    assert torch.equal(B, B.T), "polynomial output must be exactly symmetric"
+    Ad = A.double().cpu().numpy()
+    _bf16_close(B, b * Ad + c * (Ad @ Ad))
+
+
+@pytest.mark.parametrize("m,n", [(128, 128), (256, 768), (100, 300), (2048, 4096)])
+def test_update_exact(gpu, m, n):
+    X = _rand_bf16((m, n), 13, std=n**-0.5).to(gpu)
+    A = torch.empty((m, m), dtype=torch.bfloat16, device=gpu)
+    solve_ns_kernel_1(X, A)
+    B = torch.empty_like(A)
+    solve_ns_kernel_2(A, COEFFS[1], COEFFS[2], B)
+    out = torch.empty_like(X)
+    solve_ns_kernel_3(X, B, COEFFS[0], out)
+    torch.cuda.synchronize()
+    Xd = X.double().cpu().numpy()
+    Bd = B.double().cpu().numpy()
+    _bf16_close(out, COEFFS[0] * Xd + Bd @ Xd)
+
+
+def test_newton_shultz_step_matches_blocks(gpu):
+    X = _rand_bf16((256, 512), 14, std=512**-0.5).to(gpu)
+    out = torch.empty_like(X)
+    newton_shultz_step(X, *COEFFS, out)
+    A = torch.empty((256, 256), dtype=torch.bfloat16, device=gpu)
+    B = torch.empty_like(A)
+    ref = torch.empty_like(X)
+    solve_ns_kernel_1(X, A)
+    solve_ns_kernel_2(A, COEFFS[1], COEFFS[2], B)
+    solve_ns_kernel_3(X, B, COEFFS[0], ref)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+def _run_muon(shapes, gpu, seed=1, lr=2e-2, **kw):
+    ps, gs, ms = muon_inputs(shapes, seed=seed)
+    params = [torch.nn.Parameter(p.to(gpu)) for p in ps]
+    opt = HipMuon(params, lr=lr, coeffs=COEFFS, **kw)
+    for p, g, m in zip(params, gs, ms):
+        p.grad = g.to(gpu)
+        opt.momentum[p].copy_(m)
+    return ps, gs, ms, params, opt
+
+
+SMALL_SHAPES = [(128, 256), (256, 128), (100, 37), (37, 100), (512, 512), (640, 1280), (1, 5), (300, 1)]
+
+
+@pytest.mark.parametrize("nesterov,ns_steps", [(True, 5), (False, 5), (True, 1), (True, 0), (True, 2)])
+def test_muon_step_vs_oracle(gpu, nesterov, ns_steps):
+    shapes = SMALL_SHAPES
+    ps, gs, ms, params, opt = _run_muon(shapes, gpu, nesterov=nesterov, ns_steps=ns_steps)
+    outs = []
+    for p in params:  # update outputs through muon_step's `out` on a copy of each matrix
+        outs.append(torch.empty_like(p))
+    w2 = [p.detach().clone() for p in params]
+    mom2 = [m.to(gpu) for m in ms]
+    g2 = [g.to(gpu) for g in gs]
+    for w, g, m, o, shp in zip(w2, g2, mom2, outs, shapes):
+        muon_step(w, g, m, opt.beta, *COEFFS, opt.lr, scaled_lr(opt.lr, "original", *shp), opt.weight_decay,
+                  ns_steps, opt.eps, nesterov, out=o)
+    opt.step()
+    torch.cuda.synchronize()
+    for i, shp in enumerate(shapes):
+        ep, em, eo = oracle.muon.muon_update(ps[i].numpy(), gs[i].numpy(), ms[i].numpy(), lr=opt.lr,
+                                             weight_decay=opt.weight_decay, beta=opt.beta, nesterov=nesterov,
+                                             coeffs=COEFFS, ns_steps=ns_steps, eps=opt.eps)
+        assert np.array_equal(opt.momentum[params[i]].cpu().numpy(), em), f"momentum {shp}"
+        assert torch.equal(params[i].detach(), w2[i]), f"batched step != single muon_step {shp}"
+        upd = outs[i].cpu().numpy()
+        err = rel_fro(upd, eo)
+        assert err <= 1e-2, f"{shp}: update rel err {err}"
+        exact = oracle.muon.zeropower_ns(
+            oracle.muon.lerp(gs[i].numpy(), em, opt.beta) if nesterov else em, COEFFS, ns_steps, opt.eps,
+            exact=True)
+        assert rel_fro(upd, exact) <= 3e-2, f"{shp}: far from exact NS"
+        got = params[i].detach().cpu().numpy()
+        np.testing.assert_allclose(got, ep, atol=1e-2, rtol=1e-2)
+        # the apply epilogue itself: p*(1 - lr*wd) - slr*update, one fma in fp32
+        keep = np.float32(1 - opt.lr * opt.weight_decay)
+        slr = np.float32(scaled_lr(opt.lr, "original", *shp))
+        np.testing.assert_allclose(got, oracle.muon.fma32(-slr, upd, ps[i].numpy() * keep), rtol=0, atol=1e-7)
+
+
+def test_batched_equals_single(gpu):
+    shapes = [(256, 512)] * 3 + [(512, 256)] * 2
+    ps, gs, ms, params, opt = _run_muon(shapes, gpu, seed=4)
+    singles = []
+    for p, g, m in zip(ps, gs, ms):
+        q = torch.nn.Parameter(p.to(gpu))
+        q.grad = g.to(gpu)
+        o = HipMuon([q], lr=opt.lr, coeffs=COEFFS)
+        o.momentum[q].copy_(m)
+        o.step()
+        singles.append(q)
+    opt.step()
+    torch.cuda.synchronize()
+    for a, b in zip(params, singles):
+        assert torch.equal(a.detach(), b.detach())
+
+
+@pytest.mark.parametrize("shape", [(768, 3072), (1024, 4096), (4096, 4096), (14336, 4096)])
+def test_config3_ns_vs_torch(gpu, shape):
+    """Config 3 shapes: blend momentum (beta 0.95, Nesterov), NS in bf16 vs torch's routine on the GPU."""
+    from torch.optim._muon import _zeropower_via_newtonschulz
+
+    ps, gs, ms = muon_inputs([shape], seed=1)
+    p = torch.nn.Parameter(ps[0].to(gpu))
+    g = gs[0].to(gpu)
+    m = ms[0].to(gpu)
+    out = torch.empty_like(p)
+    w = p.detach().clone()
+    m_ref = m.clone()
+    muon_step(w, g, m, 0.95, *COEFFS, 1e-3, scaled_lr(1e-3, "original", *shape), 0.1, 5, 1e-7, True, out=out)
+    m_ref.lerp_(g, 1 - 0.95)
+    u = g.lerp(m_ref, 0.95)
+    ref = _zeropower_via_newtonschulz(u, COEFFS, 5, 1e-7).float()
+    torch.cuda.synchronize()
+    torch.testing.assert_close(m, m_ref, atol=0, rtol=2.4e-7)  # lerp with one fma: <= 2 ulp of torch's
+    err = (out - ref).norm().item() / ref.norm().item()
+    assert err <= 1e-2, f"{shape}: NS rel err vs torch {err}"

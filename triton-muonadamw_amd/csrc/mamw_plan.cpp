@@ -1,0 +1,178 @@
+// Host-side planning and validation (no HIP calls).
+#include "mamw_plan.h"
+
+#include <string.h>
+
+namespace mamw {
+
+namespace {
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Byte ranges [a, a+na) and [b, b+nb) overlap.
+bool overlap(const void* a, size_t na, const void* b, size_t nb) {
+    uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+    return na && nb && pa < pb + nb && pb < pa + na;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// AdamW
+
+int adamw_validate_tensor(const mamw_adamw_tensor& t) {
+    if (t.numel < 0 || t.numel > kMaxNumel) return MAMW_ERR_NUMEL;
+    if (t.numel == 0) return MAMW_OK;
+    if (!t.param || !t.grad || !t.exp_avg || !t.exp_avg_sq) return MAMW_ERR_NULL;
+    if (!aligned(t.param, 4) || !aligned(t.grad, 4) || !aligned(t.exp_avg, 4) ||
+        !aligned(t.exp_avg_sq, 4))
+        return MAMW_ERR_ALIGN;
+    // param, exp_avg, exp_avg_sq are written: they must not overlap each other
+    // or the gradient.
+    const size_t nb = size_t(t.numel) * sizeof(float);
+    const void* w[3] = {t.param, t.exp_avg, t.exp_avg_sq};
+    for (int i = 0; i < 3; ++i) {
+        if (overlap(w[i], nb, t.grad, nb)) return MAMW_ERR_ALIAS;
+        for (int j = i + 1; j < 3; ++j)
+            if (overlap(w[i], nb, w[j], nb)) return MAMW_ERR_ALIAS;
+    }
+    return MAMW_OK;
+}
+
+int adamw_table_bytes(int n_tensors, size_t* bytes) {
+    if (!bytes) return MAMW_ERR_NULL;
+    if (n_tensors < 0 || n_tensors > kMaxTensors) return MAMW_ERR_COUNT;
+    *bytes = size_t(n_tensors) * sizeof(AdamWRec);
+    return MAMW_OK;
+}
+
+int adamw_table_pack(const mamw_adamw_tensor* tensors, int n_tensors, void* host_table,
+                     size_t table_bytes, int64_t* n_blocks) {
+    if (!n_blocks) return MAMW_ERR_NULL;
+    if (n_tensors < 0 || n_tensors > kMaxTensors) return MAMW_ERR_COUNT;
+    if (n_tensors > 0 && (!tensors || !host_table)) return MAMW_ERR_NULL;
+    if (table_bytes < size_t(n_tensors) * sizeof(AdamWRec)) return MAMW_ERR_TABLE;
+    AdamWRec* rec = static_cast<AdamWRec*>(host_table);
+    int64_t blocks = 0;
+    for (int i = 0; i < n_tensors; ++i) {
+        const mamw_adamw_tensor& t = tensors[i];
+        int st = adamw_validate_tensor(t);
+        if (st != MAMW_OK) return st;
+        AdamWRec r;
+        memset(&r, 0, sizeof(r));
+        r.p = t.param;
+        r.g = t.grad;
+        r.m = t.exp_avg;
+        r.v = t.exp_avg_sq;
+        r.numel = t.numel;
+        r.block_begin = blocks;
+        r.vec_ok = aligned(t.param, 16) && aligned(t.grad, 16) && aligned(t.exp_avg, 16) &&
+                   aligned(t.exp_avg_sq, 16);
+        memcpy(&rec[i], &r, sizeof(r));
+        blocks += (t.numel + kAdamWChunk - 1) / kAdamWChunk;
+        if (blocks > int64_t(0x7fffffff)) return MAMW_ERR_NUMEL;  // grid.x limit
+    }
+    *n_blocks = blocks;
+    return MAMW_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Muon
+
+int choose_tile(int64_t m, int batch) {
+    (void)batch;
+    // 256x256 tiles need 16 x 16 tiles of 256 to fill 256 CUs with a few
+    // matrices; below m = 2048 the 128 tile keeps enough workgroups in flight.
+    return m >= 2048 ? 256 : 128;
+}
+
+int muon_plan(int batch, int64_t rows, int64_t cols, int ns_steps, MuonPlan* plan) {
+    if (!plan) return MAMW_ERR_NULL;
+    if (batch < 1 || batch > MAMW_MUON_MAX_BATCH) return MAMW_ERR_COUNT;
+    if (rows < 1 || cols < 1 || rows > kMaxDim || cols > kMaxDim) return MAMW_ERR_SHAPE;
+    if (ns_steps < 0 || ns_steps >= 100) return MAMW_ERR_HYPER;
+    MuonPlan p;
+    memset(&p, 0, sizeof(p));
+    p.batch = batch;
+    p.m = rows < cols ? rows : cols;
+    p.n = rows < cols ? cols : rows;
+    p.tile = choose_tile(p.m, batch);
+    p.mp = round_up(p.m, p.tile);
+    p.np = round_up(p.n, p.tile);
+    if (p.mp * p.np > kMaxMatElems) return MAMW_ERR_SHAPE;
+    p.prep_tiles = (p.mp / kPrepTile) * (p.np / kPrepTile);
+    const size_t B = size_t(batch);
+    const size_t xe = size_t(p.mp) * size_t(p.np);  // elements of X / XT
+    const size_t ae = size_t(p.mp) * size_t(p.mp);  // elements of A / B
+    size_t off = 0;
+    p.off_x = off;
+    off = align_ws(off + B * xe * 2);
+    p.off_xt0 = off;
+    off = align_ws(off + B * xe * 2);
+    p.off_xt1 = off;
+    if (ns_steps >= 2) off = align_ws(off + B * xe * 2);
+    p.off_a = off;
+    if (ns_steps >= 1) off = align_ws(off + B * ae * 2);
+    p.off_b = off;
+    if (ns_steps >= 1) off = align_ws(off + B * ae * 2);
+    p.off_part = off;
+    off = align_ws(off + B * size_t(p.prep_tiles) * 4);
+    p.off_inv = off;
+    off = align_ws(off + B * 4);
+    p.bytes = off;
+    *plan = p;
+    return MAMW_OK;
+}
+
+int muon_validate(const mamw_muon_matrix* mats, int batch, int ns_steps, const void* workspace,
+                  size_t workspace_bytes, MuonPlan* plan, MuonBatchDescs* descs) {
+    if (!mats || !plan || !descs) return MAMW_ERR_NULL;
+    if (batch < 1 || batch > MAMW_MUON_MAX_BATCH) return MAMW_ERR_COUNT;
+    int st = muon_plan(batch, mats[0].rows, mats[0].cols, ns_steps, plan);
+    if (st != MAMW_OK) return st;
+    if (!workspace) return MAMW_ERR_WORKSPACE;
+    if (!aligned(workspace, kWsAlign) || workspace_bytes < plan->bytes) return MAMW_ERR_WORKSPACE;
+    memset(descs, 0, sizeof(*descs));
+    for (int i = 0; i < batch; ++i) {
+        const mamw_muon_matrix& M = mats[i];
+        if (M.reserved != 0) return MAMW_ERR_HYPER;
+        if (M.rows < 1 || M.cols < 1) return MAMW_ERR_SHAPE;
+        const int64_t mi = M.rows < M.cols ? M.rows : M.cols;
+        const int64_t ni = M.rows < M.cols ? M.cols : M.rows;
+        if (mi != plan->m || ni != plan->n) return MAMW_ERR_SHAPE;
+        if (!M.param || !M.grad || !M.momentum) return MAMW_ERR_NULL;
+        if (!aligned(M.param, 4) || !aligned(M.grad, 4) || !aligned(M.momentum, 4))
+            return MAMW_ERR_ALIGN;
+        const size_t nb = size_t(M.rows) * size_t(M.cols) * 4;
+        if (overlap(M.param, nb, M.grad, nb) || overlap(M.param, nb, M.momentum, nb) ||
+            overlap(M.momentum, nb, M.grad, nb))
+            return MAMW_ERR_ALIAS;
+        if (overlap(M.param, nb, workspace, plan->bytes) ||
+            overlap(M.momentum, nb, workspace, plan->bytes) ||
+            overlap(M.grad, nb, workspace, plan->bytes))
+            return MAMW_ERR_ALIAS;
+        if (M.update) {
+            if (!aligned(M.update, 4)) return MAMW_ERR_ALIGN;
+            if (overlap(M.update, nb, M.param, nb) || overlap(M.update, nb, M.grad, nb) ||
+                overlap(M.update, nb, M.momentum, nb) || overlap(M.update, nb, workspace, plan->bytes))
+                return MAMW_ERR_ALIAS;
+        }
+        for (int j = 0; j < i; ++j) {  // two entries updating the same memory race
+            const size_t nj = size_t(mats[j].rows) * size_t(mats[j].cols) * 4;
+            if (overlap(M.param, nb, mats[j].param, nj) || overlap(M.momentum, nb, mats[j].momentum, nj))
+                return MAMW_ERR_ALIAS;
+        }
+        MuonMatDesc& d = descs->d[i];
+        d.param = M.param;
+        d.grad = M.grad;
+        d.mom = M.momentum;
+        d.upd = M.update;
+        d.rows = M.rows;
+        d.cols = M.cols;
+        d.slr = M.scaled_lr;
+        d.tall = M.rows > M.cols ? 1 : 0;
+    }
+    return MAMW_OK;
+}
+
+}  // namespace mamw

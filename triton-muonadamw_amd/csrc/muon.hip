@@ -1,0 +1,633 @@
+// Muon step for gfx950: momentum -> Newton-Schulz (bf16 MFMA) -> update.
+//
+// Launch sequence for one batch of equal-shaped matrices (mamw_muon_step):
+//   1. muon_prep_kernel   momentum lerp, Nesterov blend, bf16 cast, tall-matrix
+//                         transpose; writes X (m x n) and XT (n x m) zero-padded,
+//                         and one fp32 sum of squares per 64x64 tile.
+//   2. muon_norm_kernel   fixed-order reduction of those partials ->
+//                         inv[b] = 1 / max(bf16(||X||_F), eps).
+//   3. ns_steps x { GRAM: A = X X^T,  POLY: B = b A + c A A,  UPDATE: X = a X + B X }
+//      The first iteration scales X by inv[b] as it is loaded (bf16(x * inv), the
+//      rounding point of torch's div_), the last iteration's UPDATE is APPLY:
+//      its epilogue transposes back and writes param = param*(1-lr*wd) - slr*X.
+// All GEMMs are C = A_op * B_op^T over operands stored row-major with the
+// reduction index contiguous (X for the Gram, A for A A since A is symmetric,
+// B and XT for B X), so one MFMA tile kernel serves every product.
+#include "mamw_device.h"
+#include "mamw_launch.h"
+
+namespace mamw {
+namespace {
+
+constexpr int kGemmThreads = 256;
+constexpr int kBK = 64;
+
+enum GemmMode { MODE_GRAM = 0, MODE_POLY = 1, MODE_UPDATE = 2, MODE_APPLY = 3 };
+
+// ---------------------------------------------------------------------------
+// Prep: one 64 x 64 tile of X (in X coordinates) per block.
+
+struct PrepArgs {
+    uint16_t* x;    // [batch][mp][np]
+    uint16_t* xt;   // [batch][np][mp]
+    float* part;    // [batch][prep_tiles]
+    int64_t mp, np;
+    int64_t prep_tiles;
+    int tiles_j;    // np / 64
+    float w_mom;    // 1 - beta   (lerp weight of the momentum update)
+    float w_nest;   // beta       (lerp weight of the Nesterov blend)
+};
+
+template <bool NESTEROV>
+__global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs descs, const PrepArgs a) {
+    __shared__ uint16_t tileT[64][64 + 2];
+    __shared__ float red[4];
+    const int tid = threadIdx.x;
+    const int bat = blockIdx.y;
+    const MuonMatDesc& d = descs.d[bat];
+    const int64_t q = blockIdx.x;
+    const int64_t i0 = (q / a.tiles_j) * 64, j0 = (q % a.tiles_j) * 64;
+    const bool tall = d.tall != 0;
+    // Tile origin in parameter coordinates.
+    const int64_t r0 = tall ? j0 : i0, c0 = tall ? i0 : j0;
+    const int64_t R = d.rows, C = d.cols;
+    // "Natural" output holds bf16(u) in parameter orientation, the other its transpose.
+    uint16_t* N = tall ? a.xt + bat * a.np * a.mp : a.x + bat * a.mp * a.np;
+    uint16_t* T = tall ? a.x + bat * a.mp * a.np : a.xt + bat * a.np * a.mp;
+    const int64_t ldN = tall ? a.mp : a.np, ldT = tall ? a.np : a.mp;
+
+    const int cg = tid & 15, rr = tid >> 4;
+    const int64_t c = c0 + cg * 4;
+    const bool vec = ((C & 3) == 0) && ((reinterpret_cast<uintptr_t>(d.grad) | reinterpret_cast<uintptr_t>(d.mom)) & 15) == 0;
+    float ss = 0.f;
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+        const int rl = rr + 16 * pass;
+        const int64_t r = r0 + rl;
+        float u[4] = {0.f, 0.f, 0.f, 0.f};
+        if (r < R && c < C) {
+            const int64_t off = r * C + c;
+            if (vec && c + 3 < C) {
+                const float4 g4 = *reinterpret_cast<const float4*>(d.grad + off);
+                float4 m4 = *reinterpret_cast<const float4*>(d.mom + off);
+                const float g[4] = {g4.x, g4.y, g4.z, g4.w};
+                float m[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    m[e] = lerp_torch(m[e], g[e], a.w_mom);
+                    u[e] = NESTEROV ? lerp_torch(g[e], m[e], a.w_nest) : m[e];
+                }
+                m4 = make_float4(m[0], m[1], m[2], m[3]);
+                *reinterpret_cast<float4*>(d.mom + off) = m4;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (c + e < C) {
+                        const float g = d.grad[off + e];
+                        const float m = lerp_torch(d.mom[off + e], g, a.w_mom);
+                        d.mom[off + e] = m;
+                        u[e] = NESTEROV ? lerp_torch(g, m, a.w_nest) : m;
+                    }
+                }
+            }
+        }
+        uint32_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            h[e] = f32_to_bf16(u[e]);
+            const float xb = bf16_to_f32(h[e]);
+            ss += xb * xb;
+            tileT[cg * 4 + e][rl] = uint16_t(h[e]);
+        }
+        uint2 pk;
+        pk.x = h[0] | (h[1] << 16);
+        pk.y = h[2] | (h[3] << 16);
+        *reinterpret_cast<uint2*>(N + r * ldN + c) = pk;
+    }
+    // Deterministic block sum of squares.
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    if (tid == 0) a.part[bat * a.prep_tiles + q] = (red[0] + red[1]) + (red[2] + red[3]);
+    // Transposed write: row (c0 + tr) of T, 16 consecutive elements per thread.
+    const int tr = tid >> 2, seg = (tid & 3) * 16;
+    uint4 v0, v1;
+    uint32_t w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w[k] = uint32_t(tileT[tr][seg + 2 * k]) | (uint32_t(tileT[tr][seg + 2 * k + 1]) << 16);
+    v0 = make_uint4(w[0], w[1], w[2], w[3]);
+    v1 = make_uint4(w[4], w[5], w[6], w[7]);
+    uint16_t* dst = T + (c0 + tr) * ldT + r0 + seg;
+    reinterpret_cast<uint4*>(dst)[0] = v0;
+    reinterpret_cast<uint4*>(dst)[1] = v1;
+}
+
+// inv[b] = 1 / bf16(max(bf16(sqrt(sum of squares)), eps)), the value torch
+// divides by in X.div_(X.norm().clamp(min=eps)) for a bf16 X.
+__global__ __launch_bounds__(256) void muon_norm_kernel(const float* __restrict__ part, int64_t P,
+                                                        float eps, float* __restrict__ inv) {
+    __shared__ float red[4];
+    const int tid = threadIdx.x, bat = blockIdx.x;
+    const float* p = part + bat * P;
+    float s = 0.f;
+    for (int64_t i = tid; i < P; i += 256) s += p[i];
+    s = wave_sum(s);
+    if ((tid & 63) == 0) red[tid >> 6] = s;
+    __syncthreads();
+    if (tid == 0) {
+        const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+        const float nrm = bf16_to_f32(f32_to_bf16(sqrtf(tot)));
+        const float clamped = bf16_to_f32(f32_to_bf16(fmaxf(nrm, eps)));
+        inv[bat] = 1.0f / clamped;
+    }
+}
+
+// ns_steps == 0: the update is the normalised X itself.
+__global__ __launch_bounds__(256) void muon_apply0_kernel(const MuonBatchDescs descs, const PrepArgs a,
+                                                          const float* __restrict__ inv, float keep) {
+    const int bat = blockIdx.y;
+    const MuonMatDesc& d = descs.d[bat];
+    const bool tall = d.tall != 0;
+    const uint16_t* N = tall ? a.xt + bat * a.np * a.mp : a.x + bat * a.mp * a.np;
+    const int64_t ldN = tall ? a.mp : a.np;
+    const int64_t total = d.rows * d.cols;
+    const float s = inv[bat];
+    for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
+        const int64_t r = e / d.cols, c = e % d.cols;
+        const float u = bf16_to_f32(f32_to_bf16(bf16_to_f32(N[r * ldN + c]) * s));
+        d.param[e] = __builtin_fmaf(-d.slr, u, d.param[e] * keep);
+        if (d.upd) d.upd[e] = u;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// MFMA GEMM: C[i][j] = sum_k Aop[i][k] * Bop[j][k]  (bf16 in, fp32 accumulate).
+//
+// Block tile BM x BM, 4 waves in a 2 x 2 layout, each wave a (BM/2) x (BM/2)
+// sub-tile built from v_mfma_f32_32x32x16_bf16.  K advances in steps of 64
+// through double-buffered LDS; the next step's global loads are in flight
+// while the current step's MFMAs run.  LDS rows are 128 bytes with the 16-byte
+// chunk index XOR-swizzled by (row & 7), so both the row-wise stores and the
+// 32-rows-per-instruction fragment reads are bank-conflict free.
+
+struct GemmArgs {
+    const uint16_t* aop;  // A operand, batch 0 (rows i)
+    const uint16_t* bop;  // B operand, batch 0 (rows j)
+    int64_t a_bs, b_bs;   // batch strides (elements)
+    int64_t lda, ldb;
+    int K;                // multiple of 64
+    int tiles_m, tiles_n;
+    uint16_t* c;          // GRAM/POLY: symmetric output; UPDATE: X
+    int64_t c_bs, ldc;
+    uint16_t* ct;         // UPDATE: X^T (may be NULL in the standalone entry)
+    int64_t ct_bs, ldct;
+    const uint16_t* src;  // POLY: A;  UPDATE/APPLY: X^T (read transposed as X)
+    int64_t src_bs, lds;
+    float alpha;          // coefficient on the accumulator
+    float beta;           // coefficient on src
+    const float* inv;     // per-matrix operand scale (SCALE_IN)
+    float keep;           // APPLY: 1 - lr * weight_decay
+    int64_t m, n;         // APPLY: valid extent of X
+};
+
+template <int BM, int MODE, bool SCALE_IN>
+__global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs g, const MuonBatchDescs descs) {
+    constexpr int BN = BM;
+    constexpr int WT = BM / 2;   // wave tile edge
+    constexpr int F = WT / 32;   // 32x32 fragments per wave edge
+    constexpr int AV = BM * kBK / 8 / kGemmThreads;  // 16-byte vectors per thread per operand
+    constexpr bool SYM = (MODE == MODE_GRAM || MODE == MODE_POLY);
+    constexpr int STAGE = (BM + BN) * kBK;           // bf16 elements per LDS stage
+    __shared__ uint4 smem_v[2 * STAGE / 8];
+    uint16_t* smem = reinterpret_cast<uint16_t*>(smem_v);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int bat = blockIdx.y;
+    int ti, tj;
+    if (SYM) {
+        int q = blockIdx.x, T = g.tiles_m;
+        ti = 0;
+        while (q >= T - ti) {
+            q -= T - ti;
+            ++ti;
+        }
+        tj = ti + q;
+    } else {
+        ti = blockIdx.x / g.tiles_n;
+        tj = blockIdx.x % g.tiles_n;
+    }
+    const uint16_t* Ag = g.aop + bat * g.a_bs + int64_t(ti) * BM * g.lda;
+    const uint16_t* Bg = g.bop + bat * g.b_bs + int64_t(tj) * BN * g.ldb;
+    const float sc = SCALE_IN ? g.inv[bat] : 1.0f;
+
+    uint4 ra[AV], rb[AV];
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int v = 0; v < AV; ++v) {
+            const int idx = v * kGemmThreads + tid, row = idx >> 3, ch = idx & 7;
+            ra[v] = *reinterpret_cast<const uint4*>(Ag + row * g.lda + k0 + ch * 8);
+            rb[v] = *reinterpret_cast<const uint4*>(Bg + row * g.ldb + k0 + ch * 8);
+        }
+    };
+    auto sstore = [&](int buf) {
+        uint16_t* As = smem + buf * STAGE;
+        uint16_t* Bs = As + BM * kBK;
+#pragma unroll
+        for (int v = 0; v < AV; ++v) {
+            const int idx = v * kGemmThreads + tid, row = idx >> 3, ch = idx & 7;
+            const int off = row * kBK + ((ch ^ (row & 7)) << 3);
+            uint4 va = ra[v], vb = rb[v];
+            // The first iteration's X enters normalised: both Gram operands are
+            // X, while B X scales only its X operand (XT), never B.
+            if (SCALE_IN && MODE == MODE_GRAM) va = scale_bf16x8(va, sc);
+            if (SCALE_IN) vb = scale_bf16x8(vb, sc);
+            *reinterpret_cast<uint4*>(As + off) = va;
+            *reinterpret_cast<uint4*>(Bs + off) = vb;
+        }
+    };
+
+    f32x16_t acc[F][F];
+#pragma unroll
+    for (int a = 0; a < F; ++a)
+#pragma unroll
+        for (int b = 0; b < F; ++b)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+
+    const int KT = g.K / kBK;
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < KT; ++kt) {
+        if (kt + 1 < KT) gload((kt + 1) * kBK);
+        const uint16_t* As = smem + (kt & 1) * STAGE;
+        const uint16_t* Bs = As + BM * kBK;
+#pragma unroll
+        for (int ks = 0; ks < kBK / 16; ++ks) {
+            const int ch = ks * 2 + (lane >> 5);
+            bf16x8_t af[F], bfr[F];
+#pragma unroll
+            for (int f = 0; f < F; ++f) {
+                const int ra_ = wm * WT + f * 32 + (lane & 31);
+                const int rb_ = wn * WT + f * 32 + (lane & 31);
+                af[f] = *reinterpret_cast<const bf16x8_t*>(As + ra_ * kBK + ((ch ^ (ra_ & 7)) << 3));
+                bfr[f] = *reinterpret_cast<const bf16x8_t*>(Bs + rb_ * kBK + ((ch ^ (rb_ & 7)) << 3));
+            }
+#pragma unroll
+            for (int a = 0; a < F; ++a)
+#pragma unroll
+                for (int b = 0; b < F; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[b], acc[a][b], 0, 0, 0);
+        }
+        if (kt + 1 < KT) sstore((kt + 1) & 1);
+        __syncthreads();
+    }
+
+    // Epilogue.  Lane holds, for fragment (a,b) and register group q (0..3),
+    // rows rbase..rbase+3 of column col.
+#pragma unroll
+    for (int a = 0; a < F; ++a) {
+#pragma unroll
+        for (int b = 0; b < F; ++b) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int64_t rbase = int64_t(ti) * BM + wm * WT + a * 32 + q * 8 + (lane >> 5) * 4;
+                const int64_t col = int64_t(tj) * BN + wn * WT + b * 32 + (lane & 31);
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = acc[a][b][q * 4 + e];
+                if (MODE == MODE_GRAM || MODE == MODE_POLY) {
+                    if (MODE == MODE_POLY) {
+                        // A is exactly symmetric: A[r][col] = A[col][r], one 8-byte load.
+                        const uint2 s2 = *reinterpret_cast<const uint2*>(g.src + bat * g.src_bs + col * g.lds + rbase);
+                        const float s[4] = {bf16_to_f32(s2.x & 0xffffu), bf16_to_f32(s2.x >> 16),
+                                            bf16_to_f32(s2.y & 0xffffu), bf16_to_f32(s2.y >> 16)};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] = __builtin_fmaf(g.alpha, v[e], g.beta * s[e]);
+                    }
+                    uint32_t h[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) h[e] = f32_to_bf16(v[e]);
+                    uint16_t* C = g.c + bat * g.c_bs;
+                    if (ti != tj) {
+                        uint2 pk;
+                        pk.x = h[0] | (h[1] << 16);
+                        pk.y = h[2] | (h[3] << 16);
+                        *reinterpret_cast<uint2*>(C + col * g.ldc + rbase) = pk;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) C[(rbase + e) * g.ldc + col] = uint16_t(h[e]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            if (rbase + e <= col) {
+                                C[(rbase + e) * g.ldc + col] = uint16_t(h[e]);
+                                C[col * g.ldc + rbase + e] = uint16_t(h[e]);
+                            }
+                        }
+                    }
+                } else {
+                    // X[r][col] = XT[col][r]: read 4 consecutive rows with one 8-byte load.
+                    const uint2 s2 = *reinterpret_cast<const uint2*>(g.src + bat * g.src_bs + col * g.lds + rbase);
+                    uint32_t xs[4] = {s2.x & 0xffffu, s2.x >> 16, s2.y & 0xffffu, s2.y >> 16};
+                    uint32_t h[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float x = bf16_to_f32(xs[e]);
+                        if (SCALE_IN) x = bf16_to_f32(f32_to_bf16(x * sc));
+                        h[e] = f32_to_bf16(__builtin_fmaf(g.beta, x, v[e]));
+                    }
+                    if (MODE == MODE_UPDATE) {
+                        uint16_t* C = g.c + bat * g.c_bs;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) C[(rbase + e) * g.ldc + col] = uint16_t(h[e]);
+                        if (g.ct) {
+                            uint2 pk;
+                            pk.x = h[0] | (h[1] << 16);
+                            pk.y = h[2] | (h[3] << 16);
+                            *reinterpret_cast<uint2*>(g.ct + bat * g.ct_bs + col * g.ldct + rbase) = pk;
+                        }
+                    } else {  // MODE_APPLY
+                        const MuonMatDesc& d = descs.d[bat];
+                        if (col < g.n) {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const int64_t r = rbase + e;
+                                if (r < g.m) {
+                                    const int64_t idx = d.tall ? col * d.cols + r : r * d.cols + col;
+                                    const float u = bf16_to_f32(h[e]);
+                                    d.param[idx] = __builtin_fmaf(-d.slr, u, d.param[idx] * g.keep);
+                                    if (d.upd) d.upd[idx] = u;
+                                }
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 transpose, 64 x 64 tiles through LDS.
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ src,
+                                                             uint16_t* __restrict__ dst, int64_t rows,
+                                                             int64_t cols, int tiles_c) {
+    __shared__ uint16_t t[64][64 + 2];
+    const int tid = threadIdx.x, bat = blockIdx.y;
+    const int64_t r0 = int64_t(blockIdx.x / tiles_c) * 64, c0 = int64_t(blockIdx.x % tiles_c) * 64;
+    const uint16_t* s = src + bat * rows * cols;
+    uint16_t* o = dst + bat * rows * cols;
+    for (int i = tid; i < 64 * 64; i += 256) {
+        const int rl = i >> 6, cl = i & 63;
+        const int64_t r = r0 + rl, c = c0 + cl;
+        t[cl][rl] = (r < rows && c < cols) ? s[r * cols + c] : uint16_t(0);
+    }
+    __syncthreads();
+    for (int i = tid; i < 64 * 64; i += 256) {
+        const int cl = i >> 6, rl = i & 63;
+        const int64_t r = r0 + rl, c = c0 + cl;
+        if (r < rows && c < cols) o[c * rows + r] = t[cl][rl];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host-side launch helpers.
+
+// `flops` is the launch's algorithmic work: batch * (m^2 n | m^3 | 2 m^2 n) on
+// the unpadded m, n for the Gram (symmetric half), polynomial and update.
+template <int MODE, bool SCALE_IN>
+hipError_t launch_gemm(int tile, const GemmArgs& g, const MuonBatchDescs& d, int batch, double flops,
+                       hipStream_t s) {
+    const unsigned tiles = (MODE == MODE_GRAM || MODE == MODE_POLY)
+                               ? unsigned(g.tiles_m) * unsigned(g.tiles_m + 1) / 2
+                               : unsigned(g.tiles_m) * unsigned(g.tiles_n);
+    dim3 grid(tiles, unsigned(batch));
+    const int32_t kid = MODE == MODE_GRAM ? K_NS_GRAM : MODE == MODE_POLY ? K_NS_POLY
+                      : MODE == MODE_UPDATE ? K_NS_UPDATE : K_NS_APPLY;
+    const int32_t variant = 2 * tile + (SCALE_IN ? 1 : 0);
+    if (tile == 256)
+        return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, SCALE_IN>, grid, dim3(kGemmThreads), s,
+                      g, d);
+    return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE, SCALE_IN>, grid, dim3(kGemmThreads), s, g,
+                  d);
+}
+
+GemmArgs gram_args(const uint16_t* X, uint16_t* A, int64_t mp, int64_t kp, int tile) {
+    GemmArgs g{};
+    g.aop = X;
+    g.bop = X;
+    g.a_bs = g.b_bs = mp * kp;
+    g.lda = g.ldb = kp;
+    g.K = int(kp);
+    g.tiles_m = g.tiles_n = int(mp / tile);
+    g.c = A;
+    g.c_bs = mp * mp;
+    g.ldc = mp;
+    g.alpha = 1.f;
+    return g;
+}
+
+GemmArgs poly_args(const uint16_t* A, uint16_t* B, int64_t mp, int tile, float b, float c) {
+    GemmArgs g{};
+    g.aop = A;
+    g.bop = A;
+    g.a_bs = g.b_bs = mp * mp;
+    g.lda = g.ldb = mp;
+    g.K = int(mp);
+    g.tiles_m = g.tiles_n = int(mp / tile);
+    g.c = B;
+    g.c_bs = mp * mp;
+    g.ldc = mp;
+    g.src = A;
+    g.src_bs = mp * mp;
+    g.lds = mp;
+    g.alpha = c;
+    g.beta = b;
+    return g;
+}
+
+// out = a X + B X with X^T = XT as operand and epilogue source.
+GemmArgs update_args(const uint16_t* B, const uint16_t* XT, uint16_t* X, uint16_t* XTn, int64_t mp,
+                     int64_t np, int tile, float a) {
+    GemmArgs g{};
+    g.aop = B;
+    g.bop = XT;
+    g.a_bs = mp * mp;
+    g.b_bs = np * mp;
+    g.lda = mp;
+    g.ldb = mp;
+    g.K = int(mp);
+    g.tiles_m = int(mp / tile);
+    g.tiles_n = int(np / tile);
+    g.c = X;
+    g.c_bs = mp * np;
+    g.ldc = np;
+    g.ct = XTn;
+    g.ct_bs = np * mp;
+    g.ldct = mp;
+    g.src = XT;
+    g.src_bs = np * mp;
+    g.lds = mp;
+    g.alpha = 1.f;
+    g.beta = a;
+    return g;
+}
+
+}  // namespace
+}  // namespace mamw
+
+using namespace mamw;
+
+extern "C" int mamw_muon_workspace_bytes(int batch, int64_t rows, int64_t cols, int ns_steps,
+                                         size_t* bytes) {
+    if (!bytes) return MAMW_ERR_NULL;
+    MuonPlan p;
+    int st = muon_plan(batch, rows, cols, ns_steps, &p);
+    if (st != MAMW_OK) return st;
+    *bytes = p.bytes;
+    return MAMW_OK;
+}
+
+extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr, double weight_decay,
+                              double beta, int nesterov, float a, float b, float c, int ns_steps,
+                              float eps, void* workspace, size_t workspace_bytes,
+                              mamw_stream_t stream) {
+    MuonPlan p;
+    MuonBatchDescs descs;
+    int st = muon_validate(mats, batch, ns_steps, workspace, workspace_bytes, &p, &descs);
+    if (st != MAMW_OK) return st;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    char* ws = static_cast<char*>(workspace);
+    uint16_t* X = reinterpret_cast<uint16_t*>(ws + p.off_x);
+    uint16_t* XT[2] = {reinterpret_cast<uint16_t*>(ws + p.off_xt0),
+                       reinterpret_cast<uint16_t*>(ws + p.off_xt1)};
+    uint16_t* A = reinterpret_cast<uint16_t*>(ws + p.off_a);
+    uint16_t* Bm = reinterpret_cast<uint16_t*>(ws + p.off_b);
+    float* part = reinterpret_cast<float*>(ws + p.off_part);
+    float* inv = reinterpret_cast<float*>(ws + p.off_inv);
+    // Scalars as torch forms them: lerp weights and 1 - lr*wd from double.
+    const float keep = float(1.0 - lr * weight_decay);
+
+    PrepArgs pa;
+    pa.x = X;
+    pa.xt = XT[0];
+    pa.part = part;
+    pa.mp = p.mp;
+    pa.np = p.np;
+    pa.prep_tiles = p.prep_tiles;
+    pa.tiles_j = int(p.np / kPrepTile);
+    pa.w_mom = float(1.0 - beta);
+    pa.w_nest = float(beta);
+    const double B = double(batch), m = double(p.m), n = double(p.n);
+    dim3 pgrid(unsigned(p.prep_tiles), unsigned(batch));
+    // prep: read grad, momentum; write momentum, X, XT (4 + 4 + 4 + 2 + 2 bytes per element)
+    const double prep_bytes = 16.0 * B * m * n;
+    hipError_t e = nesterov ? launch(K_MUON_PREP, 1, 0.0, prep_bytes, muon_prep_kernel<true>, pgrid, dim3(256), s,
+                                     descs, pa)
+                            : launch(K_MUON_PREP, 0, 0.0, prep_bytes, muon_prep_kernel<false>, pgrid, dim3(256), s,
+                                     descs, pa);
+    if (e != hipSuccess) return int(e);
+    e = launch(K_MUON_NORM, 0, 0.0, 4.0 * B * double(p.prep_tiles), muon_norm_kernel, dim3(unsigned(batch)),
+               dim3(256), s, static_cast<const float*>(part), p.prep_tiles, eps, inv);
+    if (e != hipSuccess) return int(e);
+
+    if (ns_steps == 0) {
+        return int(launch(K_MUON_APPLY0, 0, 0.0, 10.0 * B * m * n, muon_apply0_kernel, dim3(1024, unsigned(batch)),
+                          dim3(256), s, descs, pa, static_cast<const float*>(inv), keep));
+    }
+    const double f_gram = B * m * m * n, f_poly = B * m * m * m, f_upd = 2.0 * B * m * m * n;
+    int cur = 0;
+    for (int it = 0; it < ns_steps; ++it) {
+        const bool first = (it == 0), last = (it == ns_steps - 1);
+        GemmArgs gg = gram_args(X, A, p.mp, p.np, p.tile);
+        gg.inv = inv;
+        e = first ? launch_gemm<MODE_GRAM, true>(p.tile, gg, descs, batch, f_gram, s)
+                  : launch_gemm<MODE_GRAM, false>(p.tile, gg, descs, batch, f_gram, s);
+        if (e != hipSuccess) return int(e);
+        GemmArgs gp = poly_args(A, Bm, p.mp, p.tile, b, c);
+        e = launch_gemm<MODE_POLY, false>(p.tile, gp, descs, batch, f_poly, s);
+        if (e != hipSuccess) return int(e);
+        GemmArgs gu = update_args(Bm, XT[cur], X, last ? nullptr : XT[cur ^ 1], p.mp, p.np, p.tile, a);
+        gu.inv = inv;
+        if (last) {
+            gu.keep = keep;
+            gu.m = p.m;
+            gu.n = p.n;
+            e = first ? launch_gemm<MODE_APPLY, true>(p.tile, gu, descs, batch, f_upd, s)
+                      : launch_gemm<MODE_APPLY, false>(p.tile, gu, descs, batch, f_upd, s);
+        } else {
+            e = first ? launch_gemm<MODE_UPDATE, true>(p.tile, gu, descs, batch, f_upd, s)
+                      : launch_gemm<MODE_UPDATE, false>(p.tile, gu, descs, batch, f_upd, s);
+        }
+        if (e != hipSuccess) return int(e);
+        cur ^= 1;
+    }
+    return MAMW_OK;
+}
+
+namespace {
+int check_ns_dims(int batch, int64_t m, int64_t k) {
+    if (batch < 1 || batch > 65535) return MAMW_ERR_COUNT;
+    if (m < 128 || k < 64 || m % 128 || k % 64 || m > kMaxDim || k > kMaxDim) return MAMW_ERR_SHAPE;
+    return MAMW_OK;
+}
+bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+}  // namespace
+
+extern "C" int mamw_ns_gram(const uint16_t* X, uint16_t* A, int batch, int64_t m, int64_t k,
+                            mamw_stream_t stream) {
+    int st = check_ns_dims(batch, m, k);
+    if (st != MAMW_OK) return st;
+    if (!X || !A) return MAMW_ERR_NULL;
+    if (!al16(X) || !al16(A)) return MAMW_ERR_ALIGN;
+    const int tile = (m % 256 == 0) ? choose_tile(m, batch) : 128;
+    GemmArgs g = gram_args(X, A, m, k, tile);
+    MuonBatchDescs d{};
+    return int(launch_gemm<MODE_GRAM, false>(tile, g, d, batch, double(batch) * double(m) * double(m) * double(k),
+                                             static_cast<hipStream_t>(stream)));
+}
+
+extern "C" int mamw_ns_poly(const uint16_t* A, uint16_t* B, int batch, int64_t m, float b, float c,
+                            mamw_stream_t stream) {
+    int st = check_ns_dims(batch, m, m);
+    if (st != MAMW_OK) return st;
+    if (!A || !B) return MAMW_ERR_NULL;
+    if (!al16(A) || !al16(B)) return MAMW_ERR_ALIGN;
+    if (A == B) return MAMW_ERR_ALIAS;
+    const int tile = (m % 256 == 0) ? choose_tile(m, batch) : 128;
+    GemmArgs g = poly_args(A, B, m, tile, b, c);
+    MuonBatchDescs d{};
+    return int(launch_gemm<MODE_POLY, false>(tile, g, d, batch, double(batch) * double(m) * double(m) * double(m),
+                                             static_cast<hipStream_t>(stream)));
+}
+
+extern "C" int mamw_ns_update(const uint16_t* B, const uint16_t* X, const uint16_t* XT, uint16_t* out,
+                              uint16_t* out_t, int batch, int64_t m, int64_t n, float a,
+                              mamw_stream_t stream) {
+    int st = check_ns_dims(batch, m, n);
+    if (st != MAMW_OK) return st;
+    if (n % 128) return MAMW_ERR_SHAPE;
+    if (!B || !X || !XT || !out) return MAMW_ERR_NULL;
+    if (!al16(B) || !al16(X) || !al16(XT) || !al16(out) || (out_t && !al16(out_t))) return MAMW_ERR_ALIGN;
+    if (out_t && (out_t == XT)) return MAMW_ERR_ALIAS;
+    (void)X;  // X enters through its transpose XT (operand and epilogue source)
+    const int tile = (m % 256 == 0 && n % 256 == 0) ? choose_tile(m, batch) : 128;
+    GemmArgs g = update_args(B, XT, out, out_t, m, n, tile, a);
+    MuonBatchDescs d{};
+    return int(launch_gemm<MODE_UPDATE, false>(tile, g, d, batch,
+                                               2.0 * double(batch) * double(m) * double(m) * double(n),
+                                               static_cast<hipStream_t>(stream)));
+}
+
+extern "C" int mamw_transpose_bf16(const uint16_t* src, uint16_t* dst, int batch, int64_t rows,
+                                   int64_t cols, mamw_stream_t stream) {
+    if (batch < 1 || batch > 65535) return MAMW_ERR_COUNT;
+    if (rows < 1 || cols < 1 || rows > kMaxDim || cols > kMaxDim) return MAMW_ERR_SHAPE;
+    if (!src || !dst) return MAMW_ERR_NULL;
+    if (src == dst) return MAMW_ERR_ALIAS;
+    const int tr = int((rows + 63) / 64), tc = int((cols + 63) / 64);
+    return int(launch(K_TRANSPOSE, 0, 0.0, 4.0 * double(batch) * double(rows) * double(cols), transpose_bf16_kernel,
+                      dim3(unsigned(tr * tc), unsigned(batch)), dim3(256), static_cast<hipStream_t>(stream), src, dst,
+                      rows, cols, tc));
+}

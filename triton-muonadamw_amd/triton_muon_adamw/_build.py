@@ -1,0 +1,102 @@
+"""Build ``libmuonadamw_amd.so`` in-tree with hipcc for gfx950.
+
+The library holds the HIP kernels and the C ABI declared in
+``include/muonadamw_amd.h``.  It is built in place (next to this file) so the
+same file is what tests, ``bench.py`` and the Python package load.
+
+Usage: ``python -m triton_muon_adamw._build`` (with ``triton-muonadamw_amd`` on
+``sys.path``) or ``build()`` from Python.
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+ROOT_PKG = PKG_DIR.parent                      # triton-muonadamw_amd/
+CSRC = ROOT_PKG / "csrc"
+REPO = ROOT_PKG.parent
+INCLUDE = REPO / "include"
+BUILD_DIR = ROOT_PKG / "_build"
+LIB_NAME = "libmuonadamw_amd.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+
+ARCH = "gfx950"
+
+SOURCES = ["mamw_plan.cpp", "abi.cpp", "prof.cpp", "adamw.hip", "muon.hip"]
+
+COMMON_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    f"-I{INCLUDE}",
+    f"-I{CSRC}",
+]
+# Device code: gfx950 only; packed-fp32 instructions disabled (the compiler
+# still emits ordinary scalar and vector fp32 code).
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def _hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found: the MuonAdamW HIP library cannot be built")
+
+
+def _compile(src: Path, obj: Path, verbose: bool) -> None:
+    cmd = [_hipcc(), *COMMON_FLAGS]
+    if src.suffix == ".hip":
+        cmd += HIP_FLAGS + ["-x", "hip"]
+    else:
+        # Host-only C++: HIP runtime API headers, no device compilation.
+        cmd += ["-x", "c++", "-I/opt/rocm/include", "-D__HIP_PLATFORM_AMD__"]
+    cmd += ["-c", str(src), "-o", str(obj)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")
+    if verbose and res.stderr.strip():
+        # hipcc's host pass warns that it does not know the packed-fp32 feature.
+        lines = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln]
+        if any(ln.strip() for ln in lines):
+            print("\n".join(lines), flush=True)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source and link the shared library; returns its path."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    objs = []
+    jobs = min(len(SOURCES), max(1, os.cpu_count() or 1))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        futs = []
+        for name in SOURCES:
+            src = CSRC / name
+            obj = BUILD_DIR / (name + ".o")
+            objs.append(obj)
+            futs.append(ex.submit(_compile, src, obj, verbose))
+        for f in futs:
+            f.result()
+    tmp = LIB_PATH.with_name(LIB_NAME + ".tmp")
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

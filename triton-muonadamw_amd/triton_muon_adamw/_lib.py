@@ -1,0 +1,173 @@
+"""ctypes binding of ``libmuonadamw_amd.so`` (the C ABI in include/muonadamw_amd.h).
+
+The library is loaded once, from next to this file.  There is no fallback:
+if the library is missing every optimizer step raises, so a run never
+silently computes on another path.
+
+Status codes map to exceptions: negative (argument rejected on the host) ->
+``ValueError``; positive (a hipError_t) -> ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libmuonadamw_amd.so")
+ABI_VERSION = 1
+MUON_MAX_BATCH = 32
+
+
+class AdamWTensor(ctypes.Structure):
+    """``mamw_adamw_tensor``."""
+
+    _fields_ = [
+        ("param", c_void_p),
+        ("grad", c_void_p),
+        ("exp_avg", c_void_p),
+        ("exp_avg_sq", c_void_p),
+        ("numel", c_int64),
+    ]
+
+
+class MuonMatrix(ctypes.Structure):
+    """``mamw_muon_matrix``."""
+
+    _fields_ = [
+        ("param", c_void_p),
+        ("grad", c_void_p),
+        ("momentum", c_void_p),
+        ("update", c_void_p),
+        ("rows", c_int64),
+        ("cols", c_int64),
+        ("scaled_lr", c_float),
+        ("reserved", c_int32),
+    ]
+
+
+class ProfRecord(ctypes.Structure):
+    """``mamw_prof_record``."""
+
+    _fields_ = [
+        ("kernel", c_int32),
+        ("variant", c_int32),
+        ("flops", c_double),
+        ("bytes", c_double),
+        ("ms", c_float),
+        ("pad", c_int32),
+    ]
+
+
+_PROTOTYPES = {
+    "mamw_abi_version": (c_int, []),
+    "mamw_strerror": (c_char_p, [c_int]),
+    "mamw_adamw_tensor_step": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_float, c_float, c_float, c_float,
+         c_float, c_float, c_float, c_void_p],
+    ),
+    "mamw_adamw_table_bytes": (c_int, [c_int, POINTER(c_size_t)]),
+    "mamw_adamw_table_pack": (c_int, [POINTER(AdamWTensor), c_int, c_void_p, c_size_t, POINTER(c_int64)]),
+    "mamw_adamw_mt_step": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_float, c_float, c_float, c_float, c_float, c_float, c_float,
+         c_void_p],
+    ),
+    "mamw_muon_workspace_bytes": (c_int, [c_int, c_int64, c_int64, c_int, POINTER(c_size_t)]),
+    "mamw_muon_step": (
+        c_int,
+        [POINTER(MuonMatrix), c_int, c_double, c_double, c_double, c_int, c_float, c_float, c_float,
+         c_int, c_float, c_void_p, c_size_t, c_void_p],
+    ),
+    "mamw_ns_gram": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_int64, c_void_p]),
+    "mamw_ns_poly": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_float, c_float, c_void_p]),
+    "mamw_ns_update": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int64, c_float, c_void_p],
+    ),
+    "mamw_transpose_bf16": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_int64, c_void_p]),
+    "mamw_prof_start": (c_int, []),
+    "mamw_prof_stop": (c_int, []),
+    "mamw_prof_collect": (c_int, [POINTER(ProfRecord), c_int, POINTER(c_int)]),
+    "mamw_prof_kernel_name": (c_char_p, [c_int]),
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load the library (once) and declare every prototype."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH.name} is not built; run __graft_entry__.build() "
+            "(or python -m triton_muon_adamw._build). MuonAdamW has no fallback path.")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (res, args) in _PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.mamw_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{LIB_PATH.name} ABI {lib.mamw_abi_version()} != expected {ABI_VERSION}")
+    _lib = lib
+    return lib
+
+
+def strerror(status: int) -> str:
+    return load().mamw_strerror(status).decode()
+
+
+def check(status: int, what: str) -> None:
+    """Raise for a non-zero status returned by ``what``."""
+    if status == 0:
+        return
+    msg = f"{what}: {strerror(status)} (status {status})"
+    if status < 0:
+        raise ValueError(msg)
+    raise RuntimeError(msg)
+
+
+def require_gpu_tensor(t: torch.Tensor, name: str) -> None:
+    """The kernels run on ROCm devices only; CPU tensors are an error."""
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"{name} is on {t.device}; MuonAdamW's HIP kernels need tensors on a ROCm GPU "
+            "(there is no CPU path)")
+
+
+def stream_handle(device: torch.device) -> int:
+    """hipStream_t of torch's current stream on ``device`` (0 = null stream)."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def prof_start() -> None:
+    """Start timing every kernel launch of the library (HIP events per dispatch)."""
+    check(load().mamw_prof_start(), "mamw_prof_start")
+
+
+def prof_stop() -> None:
+    check(load().mamw_prof_stop(), "mamw_prof_stop")
+
+
+def prof_collect() -> list[dict]:
+    """Wait for the recorded launches and return one dict per launch, in launch order."""
+    lib = load()
+    count = c_int(0)
+    st = lib.mamw_prof_collect(None, 0, ctypes.byref(count))
+    if st not in (0, -8):
+        check(st, "mamw_prof_collect")
+    n = count.value
+    if n == 0:
+        return []
+    recs = (ProfRecord * n)()
+    check(lib.mamw_prof_collect(recs, n, ctypes.byref(count)), "mamw_prof_collect")
+    return [
+        {"kernel": lib.mamw_prof_kernel_name(r.kernel).decode(), "variant": r.variant, "flops": r.flops,
+         "bytes": r.bytes, "ms": r.ms}
+        for r in recs[: count.value]
+    ]

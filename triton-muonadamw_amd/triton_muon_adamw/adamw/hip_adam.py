@@ -1,0 +1,151 @@
+"""AdamW branch on the gfx950 multi-tensor kernel.
+
+Drop-in for the reference's ``TritonAdamW`` (adamw/triton_adam.py:106-161) and
+``solve_adamw_step`` (:66-103): same constructor, attributes (``model_params``,
+``beta1``, ``beta2``, ``lr``, ``weight_decay``, ``eps``, ``step_num``, ``m``,
+``v``) and step semantics:
+
+* one global ``step_num``, incremented on every ``step()`` call, also for
+  parameters whose gradient is ``None`` (triton_adam.py:137);
+* bias corrections ``1 - beta**step_num`` computed on the host in float64 and
+  handed to the kernel as float32 (:147-148);
+* parameters whose ``grad`` is ``None`` are skipped (:139-140);
+* ``zero_grad()`` zero-fills existing gradients (:155-161).
+
+Where the reference launches one kernel per parameter, ``step()`` launches
+one kernel for all of them (``mamw_adamw_mt_step``).  The packed tensor table
+lives in device memory and is rebuilt only when a parameter or gradient
+pointer changes.  Parameters may have any number of dimensions (the reference
+handles 1-D and 2-D only); they must be contiguous float32 on a ROCm device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from collections.abc import Iterable
+
+import torch
+import torch.nn as nn
+
+from .. import _lib
+
+
+def _check_tensor(t: torch.Tensor, name: str) -> None:
+    _lib.require_gpu_tensor(t, name)
+    if t.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32 (got {t.dtype})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def solve_adamw_step(matrix: torch.Tensor, gradient: torch.Tensor, m: torch.Tensor, v: torch.Tensor,
+                     lr: float, bias1: float, bias2: float, beta1: float, beta2: float,
+                     weight_decay: float, eps: float) -> None:
+    """One AdamW update of one tensor in place (triton_adam.py:66-103)."""
+    for t, name in ((matrix, "param"), (gradient, "grad"), (m, "exp_avg"), (v, "exp_avg_sq")):
+        _check_tensor(t, name)
+        if t.numel() != matrix.numel() or t.device != matrix.device:
+            raise ValueError(f"{name} must match the parameter's numel and device")
+    lib = _lib.load()
+    with torch.cuda.device(matrix.device):
+        st = lib.mamw_adamw_tensor_step(
+            matrix.data_ptr(), gradient.data_ptr(), m.data_ptr(), v.data_ptr(), matrix.numel(),
+            lr, bias1, bias2, beta1, beta2, weight_decay, eps, _lib.stream_handle(matrix.device))
+    _lib.check(st, "mamw_adamw_tensor_step")
+
+
+class _DevicePlan:
+    """Packed tensor table of one device, resident in device memory."""
+
+    __slots__ = ("device", "table", "n_tensors", "n_blocks")
+
+    def __init__(self, device: torch.device, entries: list[tuple[torch.Tensor, ...]]):
+        lib = _lib.load()
+        n = len(entries)
+        arr = (_lib.AdamWTensor * n)()
+        for i, (p, g, m, v) in enumerate(entries):
+            arr[i] = _lib.AdamWTensor(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), p.numel())
+        nbytes = ctypes.c_size_t()
+        _lib.check(lib.mamw_adamw_table_bytes(n, ctypes.byref(nbytes)), "mamw_adamw_table_bytes")
+        host = torch.empty(max(nbytes.value, 1), dtype=torch.uint8)
+        nblocks = ctypes.c_int64()
+        _lib.check(lib.mamw_adamw_table_pack(arr, n, host.data_ptr(), nbytes.value, ctypes.byref(nblocks)),
+                   "mamw_adamw_table_pack")
+        self.device = device
+        self.table = host.to(device)
+        self.n_tensors = n
+        self.n_blocks = nblocks.value
+
+
+class HipAdamW:
+    """AdamW over a list of parameters, one gfx950 kernel launch per step."""
+
+    def __init__(
+        self,
+        params: Iterable[nn.Parameter] | list[nn.Parameter],
+        lr=1e-3,
+        betas: tuple[float, float] = (0.9, 0.999),
+        weight_decay=1e-2,
+        eps=1e-7,
+    ):
+        self.model_params = list(params)
+        self.beta1 = betas[0]
+        self.beta2 = betas[1]
+        self.lr = lr
+        self.weight_decay = weight_decay
+        self.eps = eps
+        self.step_num = 0
+        self.m = {}
+        self.v = {}
+        for param in self.model_params:
+            self.m[param] = torch.zeros_like(param, dtype=torch.float32)
+            self.v[param] = torch.zeros_like(param, dtype=torch.float32)
+        self._plan_key = None
+        self._plans: list[_DevicePlan] = []
+
+    def _build_plans(self, active: list[nn.Parameter]) -> None:
+        by_dev: dict[torch.device, list] = {}
+        for p in active:
+            g = p.grad
+            _check_tensor(p, "param")
+            _check_tensor(g, "param.grad")
+            if g.shape != p.shape or g.device != p.device:
+                raise ValueError("param.grad must match the parameter's shape and device")
+            m, v = self.m[p], self.v[p]
+            _check_tensor(m, "exp_avg")
+            _check_tensor(v, "exp_avg_sq")
+            by_dev.setdefault(p.device, []).append((p, g, m, v))
+        self._plans = [_DevicePlan(dev, ents) for dev, ents in by_dev.items()]
+
+    @torch.no_grad()
+    def step(self):
+        """Performs one iteration of the AdamW optimizer step."""
+        self.step_num += 1
+        active = [p for p in self.model_params if p.grad is not None]
+        if not active:
+            return
+        key = tuple((id(p), p.data_ptr(), p.grad.data_ptr()) for p in active)
+        if key != self._plan_key:
+            self._plan_key = None
+            self._build_plans(active)
+            self._plan_key = key
+        lib = _lib.load()
+        bias1 = 1 - self.beta1**self.step_num
+        bias2 = 1 - self.beta2**self.step_num
+        for plan in self._plans:
+            with torch.cuda.device(plan.device):
+                st = lib.mamw_adamw_mt_step(
+                    plan.table.data_ptr(), plan.n_tensors, plan.n_blocks, self.lr, bias1, bias2,
+                    self.beta1, self.beta2, self.weight_decay, self.eps,
+                    _lib.stream_handle(plan.device))
+            _lib.check(st, "mamw_adamw_mt_step")
+
+    def zero_grad(self):
+        """Resets gradients back to zero."""
+        for param in self.model_params:
+            if param.grad is not None:
+                param.grad.zero_()
+
+
+# The reference's class name, for drop-in imports.
+TritonAdamW = HipAdamW

@@ -1,0 +1,321 @@
+"""Muon branch on the gfx950 kernels.
+
+Drop-in for the reference's ``TritonMuon`` (muon/triton_muon.py:375-456) and its
+launchers ``solve_ns_kernel_{1,2,3}`` (:95-117, :191-212, :281-310),
+``newton_shultz_step`` (:313-325) and ``muon_step`` (:327-372).
+
+``HipMuon.step()`` groups the matrices that have a gradient by
+``(min(R,C), max(R,C))`` and runs each group as batched launches of
+``mamw_muon_step`` (at most 32 matrices and a bounded workspace per call):
+prep (momentum, Nesterov, bf16, transpose, sum of squares), norm, then per
+Newton-Schulz iteration a Gram, a polynomial and an update GEMM, the last of
+which writes the parameters.  The reference runs about 30 launches per
+matrix; here a group of up to 32 matrices costs ``2 + 3*ns_steps`` launches.
+
+Semantics kept from the reference: the constructor signature and defaults,
+``AssertionError`` for an unknown ``adjust_lr_fn`` (:392-393) and for a
+non-2-D parameter at step time (:96-97), momentum buffers shaped like the
+parameter (:407-412), ``grad is None`` skipped (:420-421), zero-filling
+``zero_grad`` (:450-456), and weight decay with the unscaled ``lr`` (:370).
+The numerics follow torch.optim.Muon (the reference's own correctness oracle):
+see ``include/muonadamw_amd.h``.  Differences from the reference, each
+matching torch: ``match_rms_adamw`` scales by ``0.2*sqrt(max(R,C))`` (the
+reference raises ``TypeError``, :428) and ``ns_steps=0`` applies the
+normalised momentum (the reference still runs one iteration, :360).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from collections.abc import Iterable
+from typing import Literal
+
+import torch
+import torch.nn as nn
+
+from .. import _lib
+
+_ADJUST_FNS = ["original", "match_rms_adamw", "spectral_unclamped"]
+
+
+def scaled_lr(lr: float, adjust_lr_fn: str, rows: int, cols: int) -> float:
+    """Shape-dependent Muon learning rate (triton_muon.py:424-431; torch/optim/_muon.py:73-84)."""
+    if adjust_lr_fn == "original":
+        return lr * math.sqrt(max(1, rows / cols))
+    if adjust_lr_fn == "match_rms_adamw":
+        return lr * (0.2 * math.sqrt(max(rows, cols)))
+    return lr * math.sqrt(rows / cols)
+
+
+def _check_matrix(t: torch.Tensor, name: str, dtype=torch.float32) -> None:
+    _lib.require_gpu_tensor(t, name)
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _workspace_bytes(batch: int, rows: int, cols: int, ns_steps: int) -> int:
+    n = ctypes.c_size_t()
+    _lib.check(_lib.load().mamw_muon_workspace_bytes(batch, rows, cols, ns_steps, ctypes.byref(n)),
+               "mamw_muon_workspace_bytes")
+    return n.value
+
+
+# ---------------------------------------------------------------------------
+# Standalone launchers (bf16 matrices).  The kernels need dimensions padded to
+# multiples of 128 (reduction length: 64); inputs that are not are copied into
+# zero-padded buffers, which leaves every product unchanged.
+
+def _padded(x: torch.Tensor, rows: int, cols: int) -> torch.Tensor:
+    if x.shape == (rows, cols) and x.is_contiguous():
+        return x
+    out = torch.zeros((rows, cols), dtype=x.dtype, device=x.device)
+    out[: x.shape[0], : x.shape[1]] = x
+    return out
+
+
+def _rup(x: int, to: int) -> int:
+    return (x + to - 1) // to * to
+
+
+def _check_bf16_2d(x: torch.Tensor, name: str) -> None:
+    if x.ndim != 2:
+        raise AssertionError("Muon only supports 2D tensors")
+    _lib.require_gpu_tensor(x, name)
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"{name} must be bfloat16 (got {x.dtype})")
+
+
+def solve_ns_kernel_1(matrix: torch.Tensor, out: torch.Tensor) -> None:
+    """out = matrix @ matrix.T for a bf16 m x k matrix (triton_muon.py:95-117)."""
+    _check_bf16_2d(matrix, "matrix")
+    m, k = matrix.shape
+    mp, kp = _rup(m, 128), _rup(k, 64)
+    X = _padded(matrix, mp, kp)
+    A = torch.empty((mp, mp), dtype=torch.bfloat16, device=matrix.device)
+    lib = _lib.load()
+    with torch.cuda.device(matrix.device):
+        st = lib.mamw_ns_gram(X.data_ptr(), A.data_ptr(), 1, mp, kp, _lib.stream_handle(matrix.device))
+    _lib.check(st, "mamw_ns_gram")
+    out.copy_(A[:m, :m])
+
+
+def solve_ns_kernel_2(matrix: torch.Tensor, b: float, c: float, out: torch.Tensor) -> None:
+    """out = b*A + c*(A @ A.T) for a symmetric bf16 m x m matrix A (triton_muon.py:191-212)."""
+    _check_bf16_2d(matrix, "matrix")
+    m = matrix.shape[0]
+    mp = _rup(m, 128)
+    A = _padded(matrix, mp, mp)
+    B = torch.empty((mp, mp), dtype=torch.bfloat16, device=matrix.device)
+    lib = _lib.load()
+    with torch.cuda.device(matrix.device):
+        st = lib.mamw_ns_poly(A.data_ptr(), B.data_ptr(), 1, mp, b, c, _lib.stream_handle(matrix.device))
+    _lib.check(st, "mamw_ns_poly")
+    out.copy_(B[:m, :m])
+
+
+def _transpose(x: torch.Tensor) -> torch.Tensor:
+    r, c = x.shape
+    t = torch.empty((c, r), dtype=x.dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        st = _lib.load().mamw_transpose_bf16(x.data_ptr(), t.data_ptr(), 1, r, c,
+                                             _lib.stream_handle(x.device))
+    _lib.check(st, "mamw_transpose_bf16")
+    return t
+
+
+def solve_ns_kernel_3(X: torch.Tensor, out_2: torch.Tensor, a: float, out: torch.Tensor) -> None:
+    """out = a*X + out_2 @ X for bf16 X (m x n) and symmetric out_2 (m x m) (triton_muon.py:281-310)."""
+    _check_bf16_2d(X, "X")
+    _check_bf16_2d(out_2, "out_2")
+    m, n = X.shape
+    mp, np_ = _rup(m, 128), _rup(n, 128)
+    Xp = _padded(X, mp, np_)
+    Bp = _padded(out_2, mp, mp)
+    XT = _transpose(Xp)
+    O = torch.empty((mp, np_), dtype=torch.bfloat16, device=X.device)
+    lib = _lib.load()
+    with torch.cuda.device(X.device):
+        st = lib.mamw_ns_update(Bp.data_ptr(), Xp.data_ptr(), XT.data_ptr(), O.data_ptr(), None, 1, mp, np_,
+                                a, _lib.stream_handle(X.device))
+    _lib.check(st, "mamw_ns_update")
+    out.copy_(O[:m, :n])
+
+
+def newton_shultz_step(X: torch.Tensor, a: float, b: float, c: float, out: torch.Tensor) -> None:
+    """One Newton-Schulz iteration out = a*X + (b*A + c*A@A) @ X, A = X @ X.T (triton_muon.py:313-325)."""
+    _check_bf16_2d(X, "X")
+    m, n = X.shape
+    mp, np_ = _rup(m, 128), _rup(n, 128)
+    dev = X.device
+    Xp = _padded(X, mp, np_)
+    XT = _transpose(Xp)
+    A = torch.empty((mp, mp), dtype=torch.bfloat16, device=dev)
+    B = torch.empty((mp, mp), dtype=torch.bfloat16, device=dev)
+    O = torch.empty((mp, np_), dtype=torch.bfloat16, device=dev)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        s = _lib.stream_handle(dev)
+        _lib.check(lib.mamw_ns_gram(Xp.data_ptr(), A.data_ptr(), 1, mp, np_, s), "mamw_ns_gram")
+        _lib.check(lib.mamw_ns_poly(A.data_ptr(), B.data_ptr(), 1, mp, b, c, s), "mamw_ns_poly")
+        _lib.check(lib.mamw_ns_update(B.data_ptr(), Xp.data_ptr(), XT.data_ptr(), O.data_ptr(), None, 1, mp,
+                                      np_, a, s), "mamw_ns_update")
+    out.copy_(O[:m, :n])
+
+
+def muon_step(weights: torch.Tensor, grad: torch.Tensor, momentum: torch.Tensor, beta: float, a: float,
+              b: float, c: float, lr: float, scaled_lr: float, weight_decay: float, steps: int, eps: float,
+              nesterov: bool, out: torch.Tensor | None = None) -> None:
+    """One Muon update of one matrix in place (triton_muon.py:327-372).
+
+    ``out`` (optional, fp32, shaped like ``weights``) receives the
+    orthogonalised update, as the reference's ``out`` buffer does (:368).
+    """
+    if weights.ndim != 2:
+        raise AssertionError("Muon only supports 2D tensors")
+    for t, name in ((weights, "weights"), (grad, "grad"), (momentum, "momentum")):
+        _check_matrix(t, name)
+        if t.shape != weights.shape or t.device != weights.device:
+            raise ValueError(f"{name} must match the weights' shape and device")
+    if out is not None:
+        _check_matrix(out, "out")
+        if out.shape != weights.shape or out.device != weights.device:
+            raise ValueError("out must match the weights' shape and device")
+    R, C = weights.shape
+    nbytes = _workspace_bytes(1, R, C, steps)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=weights.device)
+    arr = (_lib.MuonMatrix * 1)()
+    arr[0] = _lib.MuonMatrix(weights.data_ptr(), grad.data_ptr(), momentum.data_ptr(),
+                             out.data_ptr() if out is not None else None, R, C, scaled_lr, 0)
+    lib = _lib.load()
+    with torch.cuda.device(weights.device):
+        st = lib.mamw_muon_step(arr, 1, lr, weight_decay, beta, int(bool(nesterov)), a, b, c, steps, eps,
+                                ws.data_ptr(), nbytes, _lib.stream_handle(weights.device))
+    _lib.check(st, "mamw_muon_step")
+
+
+class _Call:
+    """One batched ``mamw_muon_step`` launch group (matrices of one shape class)."""
+
+    __slots__ = ("device", "arr", "n", "ws_bytes", "m", "n_")
+
+    def __init__(self, device, arr, n, ws_bytes, m, n_):
+        self.device, self.arr, self.n, self.ws_bytes, self.m, self.n_ = device, arr, n, ws_bytes, m, n_
+
+
+class HipMuon:
+    """Muon over a list of 2-D parameters, batched by shape on gfx950."""
+
+    # Workspace per launch group is capped at this many bytes (the batch is
+    # split further when one group would need more).
+    workspace_limit_bytes = 8 << 30
+
+    def __init__(
+        self,
+        params: Iterable[nn.Parameter] | list[nn.Parameter],
+        lr: float = 1e-3,
+        weight_decay: float = 0.1,
+        coeffs: tuple[float, float, float] = (3.445, -4.775, 2.0315),
+        nesterov: bool = True,
+        beta: float = 0.95,
+        ns_steps: int = 5,
+        eps: float = 1e-7,
+        adjust_lr_fn: Literal["original", "match_rms_adamw", "spectral_unclamped"] = "original",
+    ):
+        if adjust_lr_fn not in _ADJUST_FNS:
+            raise AssertionError(f"Invalid adjust_lr_fn: {adjust_lr_fn}")
+        self.model_params = list(params)
+        self.a = coeffs[0]
+        self.b = coeffs[1]
+        self.c = coeffs[2]
+        self.is_nesterov = nesterov
+        self.beta = beta
+        self.lr = lr
+        self.adjust_lr_fn = adjust_lr_fn
+        self.weight_decay = weight_decay
+        self.steps = ns_steps
+        self.eps = eps
+        self.momentum = {}
+        for param in self.model_params:
+            self.momentum[param] = torch.zeros_like(param, device=param.device, dtype=param.dtype)
+        self._plan_key = None
+        self._calls: list[_Call] = []
+        self._ws: dict[torch.device, torch.Tensor] = {}
+
+    def _build_calls(self, active: list[nn.Parameter]) -> None:
+        groups: dict[tuple, list[nn.Parameter]] = {}
+        for p in active:
+            if p.ndim != 2:
+                raise AssertionError("Muon only supports 2D tensors")
+            g = p.grad
+            _check_matrix(p, "param")
+            _check_matrix(g, "param.grad")
+            if g.shape != p.shape or g.device != p.device:
+                raise ValueError("param.grad must match the parameter's shape and device")
+            _check_matrix(self.momentum[p], "momentum")
+            R, C = p.shape
+            groups.setdefault((p.device, min(R, C), max(R, C)), []).append(p)
+        calls = []
+        need: dict[torch.device, int] = {}
+        for (dev, m, n), plist in groups.items():
+            one = _workspace_bytes(1, m, n, self.steps)
+            cap = max(1, min(_lib.MUON_MAX_BATCH, self.workspace_limit_bytes // max(one, 1)))
+            n_sub = -(-len(plist) // cap)
+            per = -(-len(plist) // n_sub)
+            chunks, cur, seen = [], [], set()
+            for p in plist:  # a parameter listed twice goes to a later launch (launches are ordered)
+                if len(cur) == per or id(p) in seen:
+                    chunks.append(cur)
+                    cur, seen = [], set()
+                cur.append(p)
+                seen.add(id(p))
+            chunks.append(cur)
+            for chunk in chunks:
+                arr = (_lib.MuonMatrix * len(chunk))()
+                for i, p in enumerate(chunk):
+                    R, C = p.shape
+                    arr[i] = _lib.MuonMatrix(p.data_ptr(), p.grad.data_ptr(), self.momentum[p].data_ptr(), None,
+                                             R, C, scaled_lr(self.lr, self.adjust_lr_fn, R, C), 0)
+                wsb = _workspace_bytes(len(chunk), m, n, self.steps)
+                calls.append(_Call(dev, arr, len(chunk), wsb, m, n))
+                need[dev] = max(need.get(dev, 0), wsb)
+        for dev, nbytes in need.items():
+            ws = self._ws.get(dev)
+            if ws is None or ws.numel() < nbytes:
+                self._ws[dev] = None
+                self._ws[dev] = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        self._calls = calls
+
+    @torch.no_grad()
+    def step(self):
+        """Optimizer step for the Muon optimizer."""
+        active = [p for p in self.model_params if p.grad is not None]
+        if not active:
+            return
+        key = (self.lr, self.adjust_lr_fn, self.steps,
+               tuple((id(p), p.data_ptr(), p.grad.data_ptr()) for p in active))
+        if key != self._plan_key:
+            self._plan_key = None
+            self._build_calls(active)
+            self._plan_key = key
+        lib = _lib.load()
+        nest = int(bool(self.is_nesterov))
+        for call in self._calls:
+            ws = self._ws[call.device]
+            with torch.cuda.device(call.device):
+                st = lib.mamw_muon_step(call.arr, call.n, self.lr, self.weight_decay, self.beta, nest,
+                                        self.a, self.b, self.c, self.steps, self.eps, ws.data_ptr(),
+                                        ws.numel(), _lib.stream_handle(call.device))
+            _lib.check(st, "mamw_muon_step")
+
+    def zero_grad(self):
+        """Resets gradients back to zero."""
+        for param in self.model_params:
+            if param.grad is not None:
+                param.grad.zero_()
+
+
+# The reference's class name, for drop-in imports.
+TritonMuon = HipMuon

@@ -1,0 +1,271 @@
+"""The hybrid MuonAdamW optimizer and its configuration (drop-in API).
+
+Mirrors ``MuonAdamW package/triton_muon_adamw/optimizer.py``:
+
+* ``AdamConfig`` / ``MuonConfig`` (:14-67): same fields and defaults;
+* ``MuonAdamW`` (:70-175): same constructor (argument order
+  ``model_params, muon_config, adam_config, parameter_split``), the same
+  ``auto`` / ``explicit`` routing and errors (:107-130), ``.adamw``,
+  ``.muon`` and ``.param_group`` attributes, ``step`` = AdamW branch then
+  Muon branch on the current stream with no host synchronisation,
+  zero-filling ``zero_grad``, and ``state_dict`` / ``load_state_dict``
+  carrying the parameter lists (:166-175);
+* ``PyTorchMuonAdamW`` (:178-260): the torch.optim wrapper the reference
+  checks itself against (fused ``torch.optim.AdamW`` + ``torch.optim.Muon``).
+
+The branches run on gfx950 HIP kernels (``adamw.HipAdamW``, ``muon.HipMuon``).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Literal, TypeAlias
+
+import torch
+import torch.nn as nn
+
+from .adamw.hip_adam import HipAdamW
+from .muon.hip_muon import HipMuon
+
+ParameterGroups: TypeAlias = dict[str, list[nn.Parameter]]
+
+
+@dataclass
+class AdamConfig:
+    """Hyperparameters for the AdamW branch of :class:`MuonAdamW`.
+
+    Parameters
+    ----------
+    lr:
+        Learning rate used by AdamW.
+    betas:
+        Coefficients of the first- and second-moment running averages.
+    eps:
+        Term added to the denominator for numerical stability.
+    weight_decay:
+        Decoupled AdamW weight decay coefficient.
+    """
+
+    lr: float = 1e-3
+    betas: tuple[float, float] = (0.9, 0.999)
+    eps: float = 1e-7
+    weight_decay: float = 0.01
+
+
+@dataclass
+class MuonConfig:
+    """Hyperparameters for the Muon branch of :class:`MuonAdamW`.
+
+    Parameters
+    ----------
+    lr:
+        Learning rate used by Muon.
+    beta:
+        Momentum coefficient.
+    eps:
+        Lower clamp of the Frobenius norm used to normalise the update.
+    weight_decay:
+        Decoupled weight decay coefficient (applied with the unscaled ``lr``).
+    coeffs:
+        Coefficients (a, b, c) of the Newton-Schulz polynomial.
+    nesterov:
+        Whether to use Nesterov momentum.
+    ns_steps:
+        Number of Newton-Schulz iterations.
+    adjust_lr_fn:
+        Learning-rate scaling by matrix shape.
+    """
+
+    lr: float = 1e-3
+    beta: float = 0.95
+    eps: float = 1e-7
+    weight_decay: float = 0.1
+    coeffs: tuple[float, float, float] = (3.445, -4.775, 2.0315)
+    nesterov: bool = True
+    ns_steps: int = 5
+    adjust_lr_fn: Literal["original", "match_rms_adamw", "spectral_unclamped"] = "original"
+
+
+def split_parameters(
+    model_params: nn.Module | ParameterGroups,
+    parameter_split: Literal["auto", "explicit"] = "auto",
+) -> tuple[list[nn.Parameter], list[nn.Parameter]]:
+    """Route parameters to (adam, muon) lists exactly as optimizer.py:105-130.
+
+    ``explicit``: ``model_params["adam"]`` and ``model_params["muon"]`` (each
+    defaulting to ``[]``).  ``auto``: walk ``model_params.parameters()``,
+    skipping frozen parameters and storage already seen (``data_ptr`` dedupe);
+    2-D parameters go to Muon unless they are the input embedding or output
+    head weight; everything else goes to AdamW.
+    """
+    adam_params: list[nn.Parameter] = []
+    muon_params: list[nn.Parameter] = []
+    if parameter_split == "explicit" and not isinstance(model_params, dict):
+        raise ValueError(
+            "When parameter_split is 'explicit', params must be a dictionary with keys 'adam' and 'muon' "
+            "and their corresponding parameters.")
+    if parameter_split == "auto" and isinstance(model_params, dict):
+        raise ValueError(
+            "When parameter_split is 'auto', params must be an nn.Module (ie the model itself), "
+            "not a dictionary.")
+    if parameter_split == "explicit":
+        adam_params = model_params.get("adam", [])
+        muon_params = model_params.get("muon", [])
+    elif parameter_split == "auto":
+        embed = model_params.get_input_embeddings().weight
+        head_mod = model_params.get_output_embeddings()
+        head = head_mod.weight if head_mod is not None else None
+        seen_ptrs = set()
+        for p in model_params.parameters():
+            if not p.requires_grad or p.data_ptr() in seen_ptrs:
+                continue
+            seen_ptrs.add(p.data_ptr())
+            if p.ndim == 2 and p is not embed and p is not head:
+                muon_params.append(p)
+            else:
+                adam_params.append(p)
+    return adam_params, muon_params
+
+
+class MuonAdamW(HipMuon, HipAdamW):
+    """Hybrid optimizer: Muon for 2-D weight matrices, AdamW for the rest.
+
+    Two-dimensional parameters are updated with Muon, except the input
+    embedding and the output head; all other trainable parameters (biases,
+    normalisation weights, embeddings) use the AdamW branch.
+
+    Parameters
+    ----------
+    model_params:
+        The model (``parameter_split="auto"``; it must provide
+        ``get_input_embeddings()`` and ``get_output_embeddings()``), or a
+        dictionary with ``"adam"`` and ``"muon"`` parameter lists
+        (``parameter_split="explicit"``).
+    muon_config:
+        Hyperparameters of the Muon branch.
+    adam_config:
+        Hyperparameters of the AdamW branch.
+    parameter_split:
+        ``"auto"`` or ``"explicit"``.
+
+    Notes
+    -----
+    The update kernels are gfx950 HIP kernels; parameters must be contiguous
+    float32 tensors on a ROCm device when ``step()`` runs.
+    """
+
+    def __init__(
+        self,
+        model_params: nn.Module | ParameterGroups,
+        muon_config: MuonConfig = MuonConfig(),  # noqa: B008
+        adam_config: AdamConfig = AdamConfig(),  # noqa: B008
+        parameter_split: Literal["auto", "explicit"] = "auto",
+    ) -> None:
+        adam_params, muon_params = split_parameters(model_params, parameter_split)
+        self.adamw = HipAdamW(
+            params=adam_params,
+            lr=adam_config.lr,
+            betas=adam_config.betas,
+            weight_decay=adam_config.weight_decay,
+            eps=adam_config.eps,
+        )
+        self.muon = HipMuon(
+            params=muon_params,
+            lr=muon_config.lr,
+            beta=muon_config.beta,
+            eps=muon_config.eps,
+            weight_decay=muon_config.weight_decay,
+            coeffs=muon_config.coeffs,
+            nesterov=muon_config.nesterov,
+            ns_steps=muon_config.ns_steps,
+            adjust_lr_fn=muon_config.adjust_lr_fn,
+        )
+        self.param_group = {
+            "adam": self.adamw.model_params,
+            "muon": self.muon.model_params,
+        }
+
+    def step(self) -> None:
+        """Apply one update with the AdamW branch, then the Muon branch."""
+        self.adamw.step()
+        self.muon.step()
+
+    def zero_grad(self) -> None:
+        """Zero the gradients of every parameter of both branches."""
+        self.adamw.zero_grad()
+        self.muon.zero_grad()
+
+    def state_dict(self) -> dict[str, object]:
+        """The parameter lists of both branches (optimizer.py:166-168)."""
+        return self.param_group
+
+    def load_state_dict(self, state_dict: dict[str, object]) -> None:
+        """Reassign the branches' parameter lists (optimizer.py:170-175)."""
+        if "adam" in state_dict:
+            self.adamw.model_params = state_dict["adam"]
+        if "muon" in state_dict:
+            self.muon.model_params = state_dict["muon"]
+
+
+class PyTorchMuonAdamW:
+    """torch.optim reference implementation (optimizer.py:178-260).
+
+    Same routing as :class:`MuonAdamW`; delegates to ``torch.optim.AdamW``
+    (``fused=True``) and ``torch.optim.Muon``.  Unlike the reference wrapper,
+    it forwards ``MuonConfig.coeffs`` and ``MuonConfig.eps`` to
+    ``torch.optim.Muon`` (the reference drops them, :228-236, so its wrapper
+    always ran torch's defaults); with torch's default coefficients the two
+    are the same.  Runs on CPU or GPU tensors.
+    """
+
+    def __init__(
+        self,
+        model_params: nn.Module | ParameterGroups,
+        muon_config: MuonConfig = MuonConfig(),  # noqa: B008
+        adam_config: AdamConfig = AdamConfig(),  # noqa: B008
+        parameter_split: Literal["auto", "explicit"] = "auto",
+    ) -> None:
+        adam_params, muon_params = split_parameters(model_params, parameter_split)
+        self.adamw = torch.optim.AdamW(
+            params=adam_params,
+            lr=adam_config.lr,
+            betas=adam_config.betas,
+            weight_decay=adam_config.weight_decay,
+            eps=adam_config.eps,
+            fused=True,
+        )
+        self.muon = torch.optim.Muon(
+            params=muon_params,
+            lr=muon_config.lr,
+            momentum=muon_config.beta,
+            weight_decay=muon_config.weight_decay,
+            nesterov=muon_config.nesterov,
+            ns_coefficients=tuple(muon_config.coeffs),
+            eps=muon_config.eps,
+            ns_steps=muon_config.ns_steps,
+            adjust_lr_fn=muon_config.adjust_lr_fn,
+        )
+
+    def step(self) -> None:
+        """Apply one reference AdamW and Muon update."""
+        self.adamw.step()
+        self.muon.step()
+
+    def zero_grad(self) -> None:
+        """Reset gradients for both reference optimizers."""
+        self.adamw.zero_grad()
+        self.muon.zero_grad()
+
+    def state_dict(self) -> dict[str, object]:
+        """The serialized state of both torch optimizers."""
+        return {
+            "adam": self.adamw.state_dict(),
+            "muon": self.muon.state_dict(),
+        }
+
+    def load_state_dict(self, state_dict: dict[str, object]) -> None:
+        """Load a state dictionary produced by :meth:`state_dict`."""
+        if "adam" in state_dict:
+            self.adamw.load_state_dict(state_dict["adam"])
+        if "muon" in state_dict:
+            self.muon.load_state_dict(state_dict["muon"])
