@@ -1,0 +1,211 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+declared in include/muonadamw_amd.h, and rejects invalid arguments on the host
+(negative status codes) before making any HIP call.  Device pointers here are
+fake addresses: validation never dereferences them."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from triton_muon_adamw import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "muonadamw_amd.h"
+
+OK, NULL, COUNT, NUMEL, SHAPE, ALIGN, WS, HYPER, TABLE, ALIAS = 0, -1, -2, -3, -4, -5, -6, -7, -8, -9
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mamw_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_abi():
+    names = declared_functions()
+    assert "mamw_muon_step" in names and "mamw_adamw_mt_step" in names
+    assert len(names) >= 15
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in the header but not exported"
+        assert name in _lib._PROTOTYPES, f"{name} has no ctypes prototype"
+
+
+def test_version_and_strerror():
+    lib = _lib.load()
+    assert lib.mamw_abi_version() == 1
+    for code in (OK, NULL, COUNT, NUMEL, SHAPE, ALIGN, WS, HYPER, TABLE, ALIAS):
+        msg = lib.mamw_strerror(code).decode()
+        assert msg and msg != "unknown status"
+    assert lib.mamw_strerror(-1234).decode() == "unknown status"
+    with pytest.raises(ValueError, match="NULL"):
+        _lib.check(NULL, "x")
+
+
+# ---- AdamW table ---------------------------------------------------------------
+
+def _t(base, numel, stride=1 << 30):
+    return _lib.AdamWTensor(base, base + stride, base + 2 * stride, base + 3 * stride, numel)
+
+
+def _pack(tensors):
+    lib = _lib.load()
+    n = len(tensors)
+    arr = (_lib.AdamWTensor * max(n, 1))(*tensors)
+    nbytes = ctypes.c_size_t()
+    assert lib.mamw_adamw_table_bytes(n, ctypes.byref(nbytes)) == OK
+    assert nbytes.value == 64 * n
+    buf = (ctypes.c_uint8 * max(nbytes.value, 1))()
+    blocks = ctypes.c_int64(-1)
+    st = lib.mamw_adamw_table_pack(arr, n, buf, nbytes.value, ctypes.byref(blocks))
+    return st, bytes(buf), blocks.value
+
+
+def test_adamw_pack_blocks_and_records():
+    st, buf, blocks = _pack([_t(1 << 40, 4096), _t(2 << 40, 1), _t(3 << 40, 0), _t(4 << 40, 10000)])
+    assert st == OK
+    assert blocks == 1 + 1 + 0 + 3  # 4096-element chunks
+    import struct
+
+    begins = [struct.unpack_from("<q", buf, 64 * i + 40)[0] for i in range(4)]
+    assert begins == [0, 1, 2, 2]
+    vec_ok = [struct.unpack_from("<i", buf, 64 * i + 48)[0] for i in range(4)]
+    assert vec_ok == [1, 1, 1, 1]
+    st, buf, _ = _pack([_t((1 << 40) + 4, 100)])  # 4-byte aligned, not 16
+    assert st == OK and struct.unpack_from("<i", buf, 48)[0] == 0
+
+
+@pytest.mark.parametrize("bad,code", [
+    (_lib.AdamWTensor(0, 1 << 40, 2 << 40, 3 << 40, 10), NULL),
+    (_lib.AdamWTensor(1 << 40, 2 << 40, 3 << 40, 4 << 40, -1), NUMEL),
+    (_lib.AdamWTensor((1 << 40) + 2, 2 << 40, 3 << 40, 4 << 40, 10), ALIGN),
+    (_lib.AdamWTensor(1 << 40, (1 << 40) + 8, 3 << 40, 4 << 40, 10), ALIAS),  # param overlaps grad
+    (_lib.AdamWTensor(1 << 40, 2 << 40, 3 << 40, (3 << 40) + 16, 10), ALIAS),  # exp_avg overlaps exp_avg_sq
+])
+def test_adamw_pack_rejects(bad, code):
+    st, _, _ = _pack([bad])
+    assert st == code
+
+
+def test_adamw_pack_small_table_and_counts():
+    lib = _lib.load()
+    arr = (_lib.AdamWTensor * 2)(_t(1 << 40, 10), _t(2 << 40, 10))
+    buf = (ctypes.c_uint8 * 64)()
+    blocks = ctypes.c_int64()
+    assert lib.mamw_adamw_table_pack(arr, 2, buf, 64, ctypes.byref(blocks)) == TABLE
+    assert lib.mamw_adamw_table_pack(arr, -1, buf, 64, ctypes.byref(blocks)) == COUNT
+    assert lib.mamw_adamw_table_bytes(-5, ctypes.byref(ctypes.c_size_t())) == COUNT
+
+
+def test_adamw_launch_validation_before_hip():
+    lib = _lib.load()
+    args = (3e-4, 0.1, 0.05, 0.9, 0.95, 0.1, 1e-8, None)
+    assert lib.mamw_adamw_mt_step(None, 1, 5, *args) == NULL
+    assert lib.mamw_adamw_mt_step(1 << 40 | 8, 1, 5, *args) == ALIGN
+    assert lib.mamw_adamw_mt_step(1 << 40, 1, -1, *args) == NUMEL
+    assert lib.mamw_adamw_mt_step(1 << 40, 0, 5, *args) == COUNT
+    assert lib.mamw_adamw_mt_step(None, 0, 0, *args) == OK  # nothing to do: no launch
+    assert lib.mamw_adamw_tensor_step(None, None, None, None, 0, *args) == OK
+    assert lib.mamw_adamw_tensor_step(None, 1 << 40, 2 << 40, 3 << 40, 7, *args) == NULL
+
+
+# ---- Muon workspace and validation -------------------------------------------------
+
+def _ws(batch, rows, cols, steps=5):
+    n = ctypes.c_size_t()
+    st = _lib.load().mamw_muon_workspace_bytes(batch, rows, cols, steps, ctypes.byref(n))
+    return st, n.value
+
+
+def _rup(x, t):
+    return (x + t - 1) // t * t
+
+
+@pytest.mark.parametrize("batch,rows,cols,steps", [(1, 768, 3072, 5), (24, 3072, 768, 5), (16, 14336, 4096, 5),
+                                                   (3, 100, 37, 1), (2, 5, 7, 0)])
+def test_workspace_layout(batch, rows, cols, steps):
+    st, got = _ws(batch, rows, cols, steps)
+    assert st == OK
+    m, n = min(rows, cols), max(rows, cols)
+    tile = 256 if m >= 2048 else 128
+    mp, np_ = _rup(m, tile), _rup(n, tile)
+    a = lambda x: _rup(x, 256)  # noqa: E731
+    xe = batch * mp * np_ * 2
+    ae = batch * mp * mp * 2
+    expect = a(xe) + a(xe) + (a(xe) if steps >= 2 else 0) + (2 * a(ae) if steps >= 1 else 0)
+    expect += a(batch * (mp // 64) * (np_ // 64) * 4) + a(batch * 4)
+    assert got == expect
+
+
+@pytest.mark.parametrize("args,code", [((0, 10, 10, 5), COUNT), ((33, 10, 10, 5), COUNT), ((1, 0, 10, 5), SHAPE),
+                                       ((1, 10, -3, 5), SHAPE), ((1, 10, 10, 100), HYPER), ((1, 10, 10, -1), HYPER),
+                                       ((1, 1 << 21, 10, 5), SHAPE)])
+def test_workspace_rejects(args, code):
+    assert _ws(*args)[0] == code
+
+
+def _mats(specs):
+    arr = (_lib.MuonMatrix * len(specs))()
+    for i, (r, c) in enumerate(specs):
+        base = (i + 1) << 36
+        arr[i] = _lib.MuonMatrix(base, base + (1 << 34), base + (2 << 34), None, r, c, 1e-3, 0)
+    return arr
+
+
+def _step(arr, n, ws=1 << 45, ws_bytes=1 << 40, steps=5):
+    return _lib.load().mamw_muon_step(arr, n, 1e-3, 0.1, 0.95, 1, 3.4445, -4.775, 2.0315, steps, 1e-7, ws,
+                                      ws_bytes, None)
+
+
+def test_muon_step_rejects_before_hip():
+    arr = _mats([(256, 512), (512, 300)])
+    assert _step(arr, 2) == SHAPE  # {256,512} vs {300,512}
+    arr = _mats([(256, 512), (512, 256)])
+    assert _step(arr, 2, ws=None) == WS
+    assert _step(arr, 2, ws=(1 << 45) + 64) == WS  # not 256-byte aligned
+    assert _step(arr, 2, ws_bytes=1000) == WS
+    assert _step(arr, 0) == COUNT
+    assert _step(arr, 2, steps=100) == HYPER
+    arr[1].reserved = 1
+    assert _step(arr, 2) == HYPER
+    arr = _mats([(256, 512), (512, 256)])
+    arr[1].param = arr[0].param  # two entries update the same parameter
+    assert _step(arr, 2) == ALIAS
+    arr = _mats([(256, 512)])
+    arr[0].grad = arr[0].param + 4
+    assert _step(arr, 1) == ALIAS
+    arr = _mats([(256, 512)])
+    arr[0].momentum = (1 << 45) + 4096  # inside the workspace
+    assert _step(arr, 1) == ALIAS
+    arr = _mats([(256, 512)])
+    arr[0].param = None
+    assert _step(arr, 1) == NULL
+    arr = _mats([(256, 512)])
+    arr[0].update = arr[0].param + 2
+    assert _step(arr, 1) == ALIGN
+
+
+def test_ns_blocks_validation():
+    lib = _lib.load()
+    assert lib.mamw_ns_gram(1 << 40, 2 << 40, 1, 100, 64, None) == SHAPE
+    assert lib.mamw_ns_gram(1 << 40, 2 << 40, 1, 128, 96, None) == SHAPE
+    assert lib.mamw_ns_gram(None, 2 << 40, 1, 128, 64, None) == NULL
+    assert lib.mamw_ns_gram((1 << 40) + 2, 2 << 40, 1, 128, 64, None) == ALIGN
+    assert lib.mamw_ns_poly(1 << 40, 1 << 40, 1, 128, -4.775, 2.03, None) == ALIAS
+    assert lib.mamw_ns_update(1 << 40, 2 << 40, 3 << 40, 4 << 40, 3 << 40, 1, 128, 256, 3.44, None) == ALIAS
+    assert lib.mamw_ns_update(1 << 40, 2 << 40, 3 << 40, 4 << 40, None, 1, 128, 200, 3.44, None) == SHAPE
+    assert lib.mamw_transpose_bf16(1 << 40, 1 << 40, 1, 4, 4, None) == ALIAS
+    assert lib.mamw_transpose_bf16(1 << 40, 2 << 40, 0, 4, 4, None) == COUNT
+
+
+def test_profiler_without_launches():
+    _lib.prof_start()
+    _lib.prof_stop()
+    assert _lib.prof_collect() == []
+    lib = _lib.load()
+    assert lib.mamw_prof_kernel_name(0).decode() == "adamw_mt_kernel"
+    assert lib.mamw_prof_kernel_name(99).decode() == "unknown"

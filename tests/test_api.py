@@ -1,0 +1,185 @@
+"""Drop-in API: configs, routing, errors and step semantics that need no GPU.
+
+Mirrors the behaviour of the reference's optimizer.py (configs :14-67,
+routing :105-130, errors :107-111, attributes :132-154, state_dict :166-175)
+and its branch classes (triton_adam.py:106-161, triton_muon.py:375-456).
+"""
+
+import dataclasses
+import importlib
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+import oracle
+from triton_muon_adamw import AdamConfig, MuonAdamW, MuonConfig, PyTorchMuonAdamW, split_parameters
+from triton_muon_adamw.muon.hip_muon import scaled_lr
+
+
+class TinyLM(nn.Module):
+    """Embedding + position embedding + 2 Linear + LayerNorm + head (optionally tied)."""
+
+    def __init__(self, tied=False, vocab=50, d=16):
+        super().__init__()
+        self.wte = nn.Embedding(vocab, d)
+        self.wpe = nn.Embedding(8, d)
+        self.fc = nn.Linear(d, 4 * d)
+        self.proj = nn.Linear(4 * d, d, bias=False)
+        self.ln = nn.LayerNorm(d)
+        self.head = nn.Linear(d, vocab, bias=False)
+        if tied:
+            self.head.weight = self.wte.weight
+
+    def get_input_embeddings(self):
+        return self.wte
+
+    def get_output_embeddings(self):
+        return self.head
+
+
+def test_config_defaults_match_reference():
+    a = AdamConfig()
+    assert (a.lr, a.betas, a.eps, a.weight_decay) == (1e-3, (0.9, 0.999), 1e-7, 0.01)
+    m = MuonConfig()
+    assert (m.lr, m.beta, m.eps, m.weight_decay) == (1e-3, 0.95, 1e-7, 0.1)
+    assert m.coeffs == (3.445, -4.775, 2.0315)
+    assert (m.nesterov, m.ns_steps, m.adjust_lr_fn) == (True, 5, "original")
+    assert [f.name for f in dataclasses.fields(AdamConfig)] == ["lr", "betas", "eps", "weight_decay"]
+    assert [f.name for f in dataclasses.fields(MuonConfig)] == [
+        "lr", "beta", "eps", "weight_decay", "coeffs", "nesterov", "ns_steps", "adjust_lr_fn"]
+
+
+def test_auto_routing():
+    model = TinyLM()
+    adam, muon = split_parameters(model, "auto")
+    ids = lambda ps: {id(p) for p in ps}  # noqa: E731
+    # 2-D parameters go to Muon except the input embedding and the head;
+    # the position embedding (2-D, not the input embedding) goes to Muon.
+    assert ids(muon) == ids([model.wpe.weight, model.fc.weight, model.proj.weight])
+    assert ids(adam) == ids([model.wte.weight, model.fc.bias, model.ln.weight, model.ln.bias, model.head.weight])
+    # order follows model.parameters()
+    assert [id(p) for p in muon] == [id(model.wpe.weight), id(model.fc.weight), id(model.proj.weight)]
+
+
+def test_auto_routing_tied_frozen_and_no_head():
+    model = TinyLM(tied=True)
+    model.fc.bias.requires_grad_(False)
+    adam, muon = split_parameters(model, "auto")
+    assert sum(p is model.wte.weight for p in adam) == 1  # tied head deduplicated by data_ptr
+    assert all(p is not model.fc.bias for p in adam + muon)
+    model.get_output_embeddings = lambda: None
+    adam, muon = split_parameters(model, "auto")
+    assert any(p is model.head.weight for p in adam)  # tied: same tensor as the embedding
+
+
+def test_explicit_routing_and_errors():
+    p1, p2 = nn.Parameter(torch.zeros(3, 4)), nn.Parameter(torch.zeros(4))
+    assert split_parameters({"muon": [p1]}, "explicit") == ([], [p1])
+    assert split_parameters({"adam": [p2]}, "explicit") == ([p2], [])
+    with pytest.raises(ValueError, match="explicit"):
+        split_parameters(TinyLM(), "explicit")
+    with pytest.raises(ValueError, match="auto"):
+        split_parameters({"adam": [], "muon": []}, "auto")
+    with pytest.raises(AttributeError):
+        split_parameters(nn.Linear(3, 3), "auto")
+
+
+def test_muonadamw_attributes_and_state_dict():
+    model = TinyLM()
+    opt = MuonAdamW(model, MuonConfig(lr=0.02), AdamConfig(lr=3e-4), "auto")
+    assert opt.param_group["adam"] is opt.adamw.model_params
+    assert opt.param_group["muon"] is opt.muon.model_params
+    assert opt.muon.lr == 0.02 and opt.adamw.lr == 3e-4
+    assert opt.state_dict() is opt.param_group
+    new = [nn.Parameter(torch.zeros(2, 2))]
+    opt.load_state_dict({"muon": new})
+    assert opt.muon.model_params is new
+    # state shapes: fp32 moments for AdamW, parameter-shaped momentum for Muon
+    for p in opt.adamw.model_params:
+        assert opt.adamw.m[p].shape == p.shape and opt.adamw.m[p].dtype == torch.float32
+    for p in model.fc.weight, model.proj.weight:
+        assert opt.muon.momentum[p].shape == p.shape
+
+
+def test_invalid_adjust_lr_fn_raises_assertion():
+    with pytest.raises(AssertionError, match="Invalid adjust_lr_fn"):
+        MuonAdamW(TinyLM(), MuonConfig(adjust_lr_fn="bogus"))
+
+
+def test_zero_grad_zero_fills():
+    model = TinyLM()
+    opt = MuonAdamW(model)
+    for p in model.parameters():
+        p.grad = torch.ones_like(p)
+    opt.zero_grad()
+    for p in model.parameters():
+        assert p.grad is not None and not p.grad.any()
+
+
+def test_step_on_cpu_tensors_fails_loudly():
+    model = TinyLM()
+    opt = MuonAdamW(model)
+    for p in model.parameters():
+        p.grad = torch.ones_like(p)
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        opt.step()
+    with pytest.raises(RuntimeError, match="ROCm GPU"):
+        opt.muon.step()
+
+
+def test_non_2d_muon_parameter_raises_assertion():
+    p = nn.Parameter(torch.zeros(2, 3, 4))
+    p.grad = torch.zeros_like(p)
+    opt = MuonAdamW({"muon": [p]}, parameter_split="explicit")
+    with pytest.raises(AssertionError, match="2D"):
+        opt.step()
+
+
+def test_scaled_lr_closed_forms():
+    assert scaled_lr(0.01, "original", 2048, 512) == 0.01 * 2.0
+    assert scaled_lr(0.01, "original", 512, 2048) == 0.01
+    assert scaled_lr(0.01, "match_rms_adamw", 512, 2048) == oracle.muon.adjust_lr(0.01, "match_rms_adamw",
+                                                                                    (512, 2048))
+    assert scaled_lr(0.01, "spectral_unclamped", 512, 2048) == 0.005
+
+
+def test_exports_and_shim():
+    pkg = importlib.import_module("triton_muon_adamw")
+    for name in ("AdamConfig", "MuonAdamW", "MuonConfig", "PyTorchMuonAdamW"):
+        assert name in pkg.__all__
+    from triton_muon_adamw.adamw import TritonAdamW
+    from triton_muon_adamw.muon import TritonMuon
+
+    assert issubclass(MuonAdamW, TritonMuon) and issubclass(MuonAdamW, TritonAdamW)
+    shim = importlib.import_module("MuonAdamW")
+    assert shim.MuonAdamW is MuonAdamW and shim.PyTorchMuonAdamW is PyTorchMuonAdamW
+
+
+def test_pytorch_wrapper_matches_oracle_on_cpu():
+    torch.manual_seed(0)
+    model = nn.Sequential(nn.Linear(32, 64), nn.LayerNorm(64), nn.Linear(64, 32))
+    for p in model.parameters():
+        p.grad = torch.randn_like(p) * 1e-3
+    p0 = [p.detach().numpy().copy() for p in model.parameters()]
+    g0 = [p.grad.numpy().copy() for p in model.parameters()]
+    mc = MuonConfig(lr=0.02, coeffs=(3.4445, -4.775, 2.0315))
+    ac = AdamConfig(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    split = {"adam": [p for p in model.parameters() if p.ndim == 1],
+             "muon": [p for p in model.parameters() if p.ndim == 2]}
+    ref = PyTorchMuonAdamW(split, mc, ac, "explicit")
+    ref.step()
+    for p, a, g in zip(model.parameters(), p0, g0):
+        if p.ndim == 1:
+            b1, b2 = oracle.adamw.bias_corrections(0.9, 0.95, 1)
+            e, _, _ = oracle.adamw.adamw_update(a, g, np.zeros_like(a), np.zeros_like(a), lr=3e-4, bias1=b1,
+                                                bias2=b2, beta1=0.9, beta2=0.95, weight_decay=0.1, eps=1e-8)
+            np.testing.assert_allclose(p.detach().numpy(), e, rtol=0, atol=1e-7)
+        else:
+            e, _, _ = oracle.muon.muon_update(a, g, np.zeros_like(a), lr=0.02, weight_decay=0.1, beta=0.95,
+                                              coeffs=mc.coeffs)
+            np.testing.assert_allclose(p.detach().numpy(), e, rtol=0, atol=0.02 * 8e-3)
+    sd = ref.state_dict()
+    assert set(sd) == {"adam", "muon"}
+    ref.load_state_dict(sd)
