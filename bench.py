@@ -226,12 +226,14 @@ def cpu_baseline(layout, seed: int = 0, budget_s: float = 30.0):
     t0 = time.perf_counter()
     opt.step()  # warm-up
     first = time.perf_counter() - t0
+    log(f"[cpu baseline] warm-up step {first:.1f} s on {torch.get_num_threads()} threads")
     times = []
     n_timed = max(1, min(3, int(budget_s / max(first, 1e-3)) - 1))
-    for _ in range(n_timed):
+    for i in range(n_timed):
         t0 = time.perf_counter()
         opt.step()
         times.append(time.perf_counter() - t0)
+        log(f"[cpu baseline] step {i + 1}/{n_timed}: {times[-1]:.2f} s")
     sample_ms = statistics.median(times) * 1e3
     n_adam = sum(math.prod(s) for _, s, b in sample if b == "adam")
     return {
