@@ -49,8 +49,7 @@ def kernel_label(name: str, variant: int) -> str:
     """Demangled template name of a GEMM launch as rocprofv3 reports it."""
     if name.startswith("ns_gemm_kernel:"):
         mode = name.split(":")[1]
-        tile, first = variant // 2, variant % 2
-        return f"ns_gemm_kernel<{tile}, {MODE_NUM[mode]}, {'true' if first else 'false'}>"
+        return f"ns_gemm_kernel<{variant}, {MODE_NUM[mode]}>"
     return name
 
 

@@ -21,6 +21,7 @@ enum KernelId : int32_t {
     K_MUON_PREP,
     K_MUON_NORM,
     K_MUON_APPLY0,
+    K_MUON_SCALE,
     K_NS_GRAM,
     K_NS_POLY,
     K_NS_UPDATE,

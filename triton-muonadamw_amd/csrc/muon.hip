@@ -1,15 +1,16 @@
 // Muon step for gfx950: momentum -> Newton-Schulz (bf16 MFMA) -> update.
 //
 // Launch sequence for one batch of equal-shaped matrices (mamw_muon_step):
-//   1. muon_prep_kernel   momentum lerp, Nesterov blend, bf16 cast, tall-matrix
-//                         transpose; writes X (m x n) and XT (n x m) zero-padded,
-//                         and one fp32 sum of squares per 64x64 tile.
+//   1. muon_prep_kernel   momentum lerp, Nesterov blend, bf16 cast (tall
+//                         matrices transposed through LDS); writes X (m x n,
+//                         zero-padded) and one fp32 sum of squares per 64x64 tile.
 //   2. muon_norm_kernel   fixed-order reduction of those partials ->
 //                         inv[b] = 1 / max(bf16(||X||_F), eps).
-//   3. ns_steps x { GRAM: A = X X^T,  POLY: B = b A + c A A,  UPDATE: X = a X + B X }
-//      The first iteration scales X by inv[b] as it is loaded (bf16(x * inv), the
-//      rounding point of torch's div_), the last iteration's UPDATE is APPLY:
-//      its epilogue transposes back and writes param = param*(1-lr*wd) - slr*X.
+//   3. muon_scale_kernel  X <- bf16(X * inv[b]) in place (torch's X.div_(norm)
+//                         rounding point) and XT = X^T.
+//   4. ns_steps x { GRAM: A = X X^T,  POLY: B = b A + c A A,  UPDATE: X = a X + B X }
+//      The last iteration's UPDATE is APPLY: its epilogue transposes back and
+//      writes param = param*(1-lr*wd) - slr*X.
 // All GEMMs are C = A_op * B_op^T over operands stored row-major with the
 // reduction index contiguous (X for the Gram, A for A A since A is symmetric,
 // B and XT for B X), so one MFMA tile kernel serves every product.
@@ -23,6 +24,9 @@ constexpr int kGemmThreads = 256;
 constexpr int kBK = 64;
 
 enum GemmMode { MODE_GRAM = 0, MODE_POLY = 1, MODE_UPDATE = 2, MODE_APPLY = 3 };
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 
 // ---------------------------------------------------------------------------
 // Prep: one 64 x 64 tile of X (in X coordinates) per block.
@@ -48,17 +52,15 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
     const int64_t q = blockIdx.x;
     const int64_t i0 = (q / a.tiles_j) * 64, j0 = (q % a.tiles_j) * 64;
     const bool tall = d.tall != 0;
-    // Tile origin in parameter coordinates.
+    // Tile origin in parameter coordinates (rows r, cols c of the parameter).
     const int64_t r0 = tall ? j0 : i0, c0 = tall ? i0 : j0;
     const int64_t R = d.rows, C = d.cols;
-    // "Natural" output holds bf16(u) in parameter orientation, the other its transpose.
-    uint16_t* N = tall ? a.xt + bat * a.np * a.mp : a.x + bat * a.mp * a.np;
-    uint16_t* T = tall ? a.x + bat * a.mp * a.np : a.xt + bat * a.np * a.mp;
-    const int64_t ldN = tall ? a.mp : a.np, ldT = tall ? a.np : a.mp;
+    uint16_t* X = a.x + bat * a.mp * a.np;
 
     const int cg = tid & 15, rr = tid >> 4;
     const int64_t c = c0 + cg * 4;
-    const bool vec = ((C & 3) == 0) && ((reinterpret_cast<uintptr_t>(d.grad) | reinterpret_cast<uintptr_t>(d.mom)) & 15) == 0;
+    const bool vec = ((C & 3) == 0) &&
+                     ((reinterpret_cast<uintptr_t>(d.grad) | reinterpret_cast<uintptr_t>(d.mom)) & 15) == 0;
     float ss = 0.f;
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
@@ -67,7 +69,7 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
         float u[4] = {0.f, 0.f, 0.f, 0.f};
         if (r < R && c < C) {
             const int64_t off = r * C + c;
-            if (vec && c + 3 < C) {
+            if (vec) {
                 const float4 g4 = *reinterpret_cast<const float4*>(d.grad + off);
                 float4 m4 = *reinterpret_cast<const float4*>(d.mom + off);
                 const float g[4] = {g4.x, g4.y, g4.z, g4.w};
@@ -77,8 +79,7 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
                     m[e] = lerp_torch(m[e], g[e], a.w_mom);
                     u[e] = NESTEROV ? lerp_torch(g[e], m[e], a.w_nest) : m[e];
                 }
-                m4 = make_float4(m[0], m[1], m[2], m[3]);
-                *reinterpret_cast<float4*>(d.mom + off) = m4;
+                *reinterpret_cast<float4*>(d.mom + off) = make_float4(m[0], m[1], m[2], m[3]);
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -97,29 +98,31 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
             h[e] = f32_to_bf16(u[e]);
             const float xb = bf16_to_f32(h[e]);
             ss += xb * xb;
-            tileT[cg * 4 + e][rl] = uint16_t(h[e]);
         }
-        uint2 pk;
-        pk.x = h[0] | (h[1] << 16);
-        pk.y = h[2] | (h[3] << 16);
-        *reinterpret_cast<uint2*>(N + r * ldN + c) = pk;
+        if (!tall) {  // X = bf16(u): parameter rows are X rows
+            uint2 pk;
+            pk.x = h[0] | (h[1] << 16);
+            pk.y = h[2] | (h[3] << 16);
+            *reinterpret_cast<uint2*>(X + r * a.np + c) = pk;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) tileT[cg * 4 + e][rl] = uint16_t(h[e]);
+        }
     }
-    // Deterministic block sum of squares.
     ss = wave_sum(ss);
     if ((tid & 63) == 0) red[tid >> 6] = ss;
     __syncthreads();
     if (tid == 0) a.part[bat * a.prep_tiles + q] = (red[0] + red[1]) + (red[2] + red[3]);
-    // Transposed write: row (c0 + tr) of T, 16 consecutive elements per thread.
-    const int tr = tid >> 2, seg = (tid & 3) * 16;
-    uint4 v0, v1;
-    uint32_t w[8];
+    if (tall) {  // X = bf16(u)^T: row (c0 + tr) of X, 16 consecutive elements per thread
+        const int tr = tid >> 2, seg = (tid & 3) * 16;
+        uint32_t w[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) w[k] = uint32_t(tileT[tr][seg + 2 * k]) | (uint32_t(tileT[tr][seg + 2 * k + 1]) << 16);
-    v0 = make_uint4(w[0], w[1], w[2], w[3]);
-    v1 = make_uint4(w[4], w[5], w[6], w[7]);
-    uint16_t* dst = T + (c0 + tr) * ldT + r0 + seg;
-    reinterpret_cast<uint4*>(dst)[0] = v0;
-    reinterpret_cast<uint4*>(dst)[1] = v1;
+        for (int k = 0; k < 8; ++k)
+            w[k] = uint32_t(tileT[tr][seg + 2 * k]) | (uint32_t(tileT[tr][seg + 2 * k + 1]) << 16);
+        uint4* dst = reinterpret_cast<uint4*>(X + (c0 + tr) * a.np + r0 + seg);
+        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    }
 }
 
 // inv[b] = 1 / bf16(max(bf16(sqrt(sum of squares)), eps)), the value torch
@@ -142,19 +145,46 @@ __global__ __launch_bounds__(256) void muon_norm_kernel(const float* __restrict_
     }
 }
 
+// X <- bf16(X * inv[b]) in place and XT = X^T, one 64 x 64 tile per block.
+__global__ __launch_bounds__(256) void muon_scale_kernel(const PrepArgs a, const float* __restrict__ inv) {
+    __shared__ uint16_t tileT[64][64 + 2];
+    const int tid = threadIdx.x, bat = blockIdx.y;
+    const int64_t q = blockIdx.x;
+    const int64_t i0 = (q / a.tiles_j) * 64, j0 = (q % a.tiles_j) * 64;
+    uint16_t* X = a.x + bat * a.mp * a.np;
+    uint16_t* XT = a.xt + bat * a.np * a.mp;
+    const float s = inv[bat];
+    const int cg = tid & 15, rr = tid >> 4;
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass) {
+        const int rl = rr + 16 * pass;
+        uint2* p = reinterpret_cast<uint2*>(X + (i0 + rl) * a.np + j0 + cg * 4);
+        const uint2 v = *p;
+        const uint32_t h[4] = {f32_to_bf16(bf16_to_f32(v.x & 0xffffu) * s), f32_to_bf16(bf16_to_f32(v.x >> 16) * s),
+                               f32_to_bf16(bf16_to_f32(v.y & 0xffffu) * s), f32_to_bf16(bf16_to_f32(v.y >> 16) * s)};
+        *p = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tileT[cg * 4 + e][rl] = uint16_t(h[e]);
+    }
+    __syncthreads();
+    const int tr = tid >> 2, seg = (tid & 3) * 16;
+    uint32_t w[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) w[k] = uint32_t(tileT[tr][seg + 2 * k]) | (uint32_t(tileT[tr][seg + 2 * k + 1]) << 16);
+    uint4* dst = reinterpret_cast<uint4*>(XT + (j0 + tr) * a.mp + i0 + seg);
+    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+}
+
 // ns_steps == 0: the update is the normalised X itself.
-__global__ __launch_bounds__(256) void muon_apply0_kernel(const MuonBatchDescs descs, const PrepArgs a,
-                                                          const float* __restrict__ inv, float keep) {
+__global__ __launch_bounds__(256) void muon_apply0_kernel(const MuonBatchDescs descs, const PrepArgs a, float keep) {
     const int bat = blockIdx.y;
     const MuonMatDesc& d = descs.d[bat];
-    const bool tall = d.tall != 0;
-    const uint16_t* N = tall ? a.xt + bat * a.np * a.mp : a.x + bat * a.mp * a.np;
-    const int64_t ldN = tall ? a.mp : a.np;
+    const uint16_t* X = a.x + bat * a.mp * a.np;
     const int64_t total = d.rows * d.cols;
-    const float s = inv[bat];
     for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
         const int64_t r = e / d.cols, c = e % d.cols;
-        const float u = bf16_to_f32(f32_to_bf16(bf16_to_f32(N[r * ldN + c]) * s));
+        const float u = bf16_to_f32(d.tall ? X[c * a.np + r] : X[r * a.np + c]);
         d.param[e] = __builtin_fmaf(-d.slr, u, d.param[e] * keep);
         if (d.upd) d.upd[e] = u;
     }
@@ -164,11 +194,14 @@ __global__ __launch_bounds__(256) void muon_apply0_kernel(const MuonBatchDescs d
 // MFMA GEMM: C[i][j] = sum_k Aop[i][k] * Bop[j][k]  (bf16 in, fp32 accumulate).
 //
 // Block tile BM x BM, 4 waves in a 2 x 2 layout, each wave a (BM/2) x (BM/2)
-// sub-tile built from v_mfma_f32_32x32x16_bf16.  K advances in steps of 64
-// through double-buffered LDS; the next step's global loads are in flight
-// while the current step's MFMAs run.  LDS rows are 128 bytes with the 16-byte
-// chunk index XOR-swizzled by (row & 7), so both the row-wise stores and the
-// 32-rows-per-instruction fragment reads are bank-conflict free.
+// sub-tile built from v_mfma_f32_32x32x16_bf16 (accumulators in AGPRs).  K
+// advances in steps of 64 through two LDS buffers filled straight from global
+// memory by global_load_lds_dwordx4 (no VGPR staging): the loads of step k+1
+// are issued right after the barrier that opens step k and land while step k's
+// MFMAs run.  Within a step, the fragments of the next 16-wide slice are read
+// while the current slice's MFMAs run.  LDS rows are 128 bytes with the
+// 16-byte chunk index XOR-swizzled (lds_chunk), so fragment reads are
+// bank-conflict free.
 
 struct GemmArgs {
     const uint16_t* aop;  // A operand, batch 0 (rows i)
@@ -177,6 +210,7 @@ struct GemmArgs {
     int64_t lda, ldb;
     int K;                // multiple of 64
     int tiles_m, tiles_n;
+    int tiles_per_matrix; // tiles of one matrix in the launch (upper triangle when symmetric)
     uint16_t* c;          // GRAM/POLY: symmetric output; UPDATE: X
     int64_t c_bs, ldc;
     uint16_t* ct;         // UPDATE: X^T (may be NULL in the standalone entry)
@@ -185,65 +219,92 @@ struct GemmArgs {
     int64_t src_bs, lds;
     float alpha;          // coefficient on the accumulator
     float beta;           // coefficient on src
-    const float* inv;     // per-matrix operand scale (SCALE_IN)
     float keep;           // APPLY: 1 - lr * weight_decay
     int64_t m, n;         // APPLY: valid extent of X
 };
 
-template <int BM, int MODE, bool SCALE_IN>
+// Launch block -> (matrix, tile row, tile col).  Blocks are dealt to the 8 XCDs
+// round-robin in dispatch order; the remap hands each XCD one contiguous range
+// of logical tiles (matrix-major), so the operand rows its workgroups share
+// stay in that XCD's L2.  Within a matrix, non-symmetric tiles run in groups of
+// kGroupM tile rows, column by column; symmetric ones row by row over the upper
+// triangle.
+constexpr int kXcds = 8;
+constexpr int kGroupM = 4;
+
+template <bool SYM>
+__device__ __forceinline__ void decode_tile(const GemmArgs& g, int& bat, int& ti, int& tj) {
+    const int L = blockIdx.x, total = gridDim.x;
+    const int q = total / kXcds, r = total % kXcds;
+    const int xcd = L % kXcds, j = L / kXcds;
+    const int logical = xcd < r ? xcd * (q + 1) + j : r * (q + 1) + (xcd - r) * q + j;
+    bat = logical / g.tiles_per_matrix;
+    int t = logical - bat * g.tiles_per_matrix;
+    if (SYM) {
+        const int T = g.tiles_m;
+        ti = 0;
+        while (t >= T - ti) {
+            t -= T - ti;
+            ++ti;
+        }
+        tj = ti + t;
+    } else {
+        const int width = kGroupM * g.tiles_n;
+        const int group = t / width, first = group * kGroupM;
+        const int gsize = min(g.tiles_m - first, kGroupM);
+        const int w = t - group * width;
+        ti = first + w % gsize;
+        tj = w / gsize;
+    }
+}
+
+// Physical 16-byte chunk of logical chunk `ch` (0..7) in LDS row `row` (64
+// bf16 per row).  XOR-ing with (row & 7) ^ ((row >> 3) & 1) makes any 16
+// consecutive rows at one logical chunk land on 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int lds_chunk(int row, int ch) { return ch ^ (row & 7) ^ ((row >> 3) & 1); }
+
+template <int BM, int MODE>
 __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs g, const MuonBatchDescs descs) {
     constexpr int BN = BM;
-    constexpr int WT = BM / 2;   // wave tile edge
-    constexpr int F = WT / 32;   // 32x32 fragments per wave edge
-    constexpr int AV = BM * kBK / 8 / kGemmThreads;  // 16-byte vectors per thread per operand
+    constexpr int WT = BM / 2;          // wave tile edge
+    constexpr int F = WT / 32;          // 32x32 fragments per wave edge
+    constexpr int LOADS = BM / 32;      // global_load_lds per wave per operand per step (8 rows each)
+    constexpr int STAGE = (BM + BN) * kBK;  // bf16 elements per LDS stage
     constexpr bool SYM = (MODE == MODE_GRAM || MODE == MODE_POLY);
-    constexpr int STAGE = (BM + BN) * kBK;           // bf16 elements per LDS stage
     __shared__ uint4 smem_v[2 * STAGE / 8];
     uint16_t* smem = reinterpret_cast<uint16_t*>(smem_v);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int bat = blockIdx.y;
-    int ti, tj;
-    if (SYM) {
-        int q = blockIdx.x, T = g.tiles_m;
-        ti = 0;
-        while (q >= T - ti) {
-            q -= T - ti;
-            ++ti;
-        }
-        tj = ti + q;
-    } else {
-        ti = blockIdx.x / g.tiles_n;
-        tj = blockIdx.x % g.tiles_n;
-    }
+    int bat, ti, tj;
+    decode_tile<SYM>(g, bat, ti, tj);
     const uint16_t* Ag = g.aop + bat * g.a_bs + int64_t(ti) * BM * g.lda;
     const uint16_t* Bg = g.bop + bat * g.b_bs + int64_t(tj) * BN * g.ldb;
-    const float sc = SCALE_IN ? g.inv[bat] : 1.0f;
 
-    uint4 ra[AV], rb[AV];
-    auto gload = [&](int k0) {
-#pragma unroll
-        for (int v = 0; v < AV; ++v) {
-            const int idx = v * kGemmThreads + tid, row = idx >> 3, ch = idx & 7;
-            ra[v] = *reinterpret_cast<const uint4*>(Ag + row * g.lda + k0 + ch * 8);
-            rb[v] = *reinterpret_cast<const uint4*>(Bg + row * g.ldb + k0 + ch * 8);
-        }
-    };
-    auto sstore = [&](int buf) {
+    // Wave w fills rows [w*BM/4, (w+1)*BM/4) of each operand tile, 8 rows (1 KB)
+    // per instruction: lane l lands at physical chunk l&7 of row l>>3, so it
+    // fetches the logical chunk stored there.
+    const int lrow = lane >> 3;
+    auto issue = [&](int k0, int buf) {
         uint16_t* As = smem + buf * STAGE;
         uint16_t* Bs = As + BM * kBK;
 #pragma unroll
-        for (int v = 0; v < AV; ++v) {
-            const int idx = v * kGemmThreads + tid, row = idx >> 3, ch = idx & 7;
-            const int off = row * kBK + ((ch ^ (row & 7)) << 3);
-            uint4 va = ra[v], vb = rb[v];
-            // The first iteration's X enters normalised: both Gram operands are
-            // X, while B X scales only its X operand (XT), never B.
-            if (SCALE_IN && MODE == MODE_GRAM) va = scale_bf16x8(va, sc);
-            if (SCALE_IN) vb = scale_bf16x8(vb, sc);
-            *reinterpret_cast<uint4*>(As + off) = va;
-            *reinterpret_cast<uint4*>(Bs + off) = vb;
+        for (int i = 0; i < LOADS; ++i) {
+            const int row0 = wave * (BM / 4) + i * 8, row = row0 + lrow;
+            const int ch = lds_chunk(row, lane & 7);
+            __builtin_amdgcn_global_load_lds((gbl_ptr_t)(Ag + row * g.lda + k0 + ch * 8), (lds_ptr_t)(As + row0 * kBK),
+                                             16, 0, 0);
+            __builtin_amdgcn_global_load_lds((gbl_ptr_t)(Bg + row * g.ldb + k0 + ch * 8), (lds_ptr_t)(Bs + row0 * kBK),
+                                             16, 0, 0);
+        }
+    };
+    auto frags = [&](bf16x8_t (&fa)[F], bf16x8_t (&fb)[F], const uint16_t* As, const uint16_t* Bs, int ks) {
+        const int ch = ks * 2 + (lane >> 5);
+#pragma unroll
+        for (int f = 0; f < F; ++f) {
+            const int ra = wm * WT + f * 32 + (lane & 31), rb = wn * WT + f * 32 + (lane & 31);
+            fa[f] = *reinterpret_cast<const bf16x8_t*>(As + ra * kBK + (lds_chunk(ra, ch) << 3));
+            fb[f] = *reinterpret_cast<const bf16x8_t*>(Bs + rb * kBK + (lds_chunk(rb, ch) << 3));
         }
     };
 
@@ -254,34 +315,34 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         for (int b = 0; b < F; ++b)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
+    auto mfmas = [&](const bf16x8_t (&fa)[F], const bf16x8_t (&fb)[F]) {
+#pragma unroll
+        for (int a = 0; a < F; ++a)
+#pragma unroll
+            for (int b = 0; b < F; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+    };
 
     const int KT = g.K / kBK;
-    gload(0);
-    sstore(0);
-    __syncthreads();
+    issue(0, 0);
     for (int kt = 0; kt < KT; ++kt) {
-        if (kt + 1 < KT) gload((kt + 1) * kBK);
-        const uint16_t* As = smem + (kt & 1) * STAGE;
-        const uint16_t* Bs = As + BM * kBK;
-#pragma unroll
-        for (int ks = 0; ks < kBK / 16; ++ks) {
-            const int ch = ks * 2 + (lane >> 5);
-            bf16x8_t af[F], bfr[F];
-#pragma unroll
-            for (int f = 0; f < F; ++f) {
-                const int ra_ = wm * WT + f * 32 + (lane & 31);
-                const int rb_ = wn * WT + f * 32 + (lane & 31);
-                af[f] = *reinterpret_cast<const bf16x8_t*>(As + ra_ * kBK + ((ch ^ (ra_ & 7)) << 3));
-                bfr[f] = *reinterpret_cast<const bf16x8_t*>(Bs + rb_ * kBK + ((ch ^ (rb_ & 7)) << 3));
-            }
-#pragma unroll
-            for (int a = 0; a < F; ++a)
-#pragma unroll
-                for (int b = 0; b < F; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[b], acc[a][b], 0, 0, 0);
-        }
-        if (kt + 1 < KT) sstore((kt + 1) & 1);
+        const int buf = kt & 1;
+        // Step kt's loads (own) have landed; after the barrier every wave's have,
+        // and every wave is done reading the other buffer (step kt-1).
+        __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
         __syncthreads();
+        if (kt + 1 < KT) issue((kt + 1) * kBK, buf ^ 1);
+        const uint16_t* As = smem + buf * STAGE;
+        const uint16_t* Bs = As + BM * kBK;
+        bf16x8_t fa0[F], fb0[F], fa1[F], fb1[F];
+        frags(fa0, fb0, As, Bs, 0);
+        frags(fa1, fb1, As, Bs, 1);
+        mfmas(fa0, fb0);
+        frags(fa0, fb0, As, Bs, 2);
+        mfmas(fa1, fb1);
+        frags(fa1, fb1, As, Bs, 3);
+        mfmas(fa0, fb0);
+        mfmas(fa1, fb1);
     }
 
     // Epilogue.  Lane holds, for fragment (a,b) and register group q (0..3),
@@ -329,14 +390,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
                 } else {
                     // X[r][col] = XT[col][r]: read 4 consecutive rows with one 8-byte load.
                     const uint2 s2 = *reinterpret_cast<const uint2*>(g.src + bat * g.src_bs + col * g.lds + rbase);
-                    uint32_t xs[4] = {s2.x & 0xffffu, s2.x >> 16, s2.y & 0xffffu, s2.y >> 16};
+                    const uint32_t xs[4] = {s2.x & 0xffffu, s2.x >> 16, s2.y & 0xffffu, s2.y >> 16};
                     uint32_t h[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        float x = bf16_to_f32(xs[e]);
-                        if (SCALE_IN) x = bf16_to_f32(f32_to_bf16(x * sc));
-                        h[e] = f32_to_bf16(__builtin_fmaf(g.beta, x, v[e]));
-                    }
+                    for (int e = 0; e < 4; ++e) h[e] = f32_to_bf16(__builtin_fmaf(g.beta, bf16_to_f32(xs[e]), v[e]));
                     if (MODE == MODE_UPDATE) {
                         uint16_t* C = g.c + bat * g.c_bs;
 #pragma unroll
@@ -396,21 +453,19 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
 
 // `flops` is the launch's algorithmic work: batch * (m^2 n | m^3 | 2 m^2 n) on
 // the unpadded m, n for the Gram (symmetric half), polynomial and update.
-template <int MODE, bool SCALE_IN>
+template <int MODE>
 hipError_t launch_gemm(int tile, const GemmArgs& g, const MuonBatchDescs& d, int batch, double flops,
                        hipStream_t s) {
-    const unsigned tiles = (MODE == MODE_GRAM || MODE == MODE_POLY)
-                               ? unsigned(g.tiles_m) * unsigned(g.tiles_m + 1) / 2
-                               : unsigned(g.tiles_m) * unsigned(g.tiles_n);
-    dim3 grid(tiles, unsigned(batch));
+    GemmArgs ga = g;
+    ga.tiles_per_matrix = (MODE == MODE_GRAM || MODE == MODE_POLY) ? g.tiles_m * (g.tiles_m + 1) / 2
+                                                                   : g.tiles_m * g.tiles_n;
+    dim3 grid(unsigned(ga.tiles_per_matrix) * unsigned(batch));
     const int32_t kid = MODE == MODE_GRAM ? K_NS_GRAM : MODE == MODE_POLY ? K_NS_POLY
                       : MODE == MODE_UPDATE ? K_NS_UPDATE : K_NS_APPLY;
-    const int32_t variant = 2 * tile + (SCALE_IN ? 1 : 0);
+    const int32_t variant = tile;
     if (tile == 256)
-        return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, SCALE_IN>, grid, dim3(kGemmThreads), s,
-                      g, d);
-    return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE, SCALE_IN>, grid, dim3(kGemmThreads), s, g,
-                  d);
+        return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE>, grid, dim3(kGemmThreads), s, ga, d);
+    return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE>, grid, dim3(kGemmThreads), s, ga, d);
 }
 
 GemmArgs gram_args(const uint16_t* X, uint16_t* A, int64_t mp, int64_t kp, int tile) {
@@ -521,8 +576,8 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
     pa.w_nest = float(beta);
     const double B = double(batch), m = double(p.m), n = double(p.n);
     dim3 pgrid(unsigned(p.prep_tiles), unsigned(batch));
-    // prep: read grad, momentum; write momentum, X, XT (4 + 4 + 4 + 2 + 2 bytes per element)
-    const double prep_bytes = 16.0 * B * m * n;
+    // prep: read grad, momentum; write momentum, X (4 + 4 + 4 + 2 bytes per element)
+    const double prep_bytes = 14.0 * B * m * n;
     hipError_t e = nesterov ? launch(K_MUON_PREP, 1, 0.0, prep_bytes, muon_prep_kernel<true>, pgrid, dim3(256), s,
                                      descs, pa)
                             : launch(K_MUON_PREP, 0, 0.0, prep_bytes, muon_prep_kernel<false>, pgrid, dim3(256), s,
@@ -531,34 +586,31 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
     e = launch(K_MUON_NORM, 0, 0.0, 4.0 * B * double(p.prep_tiles), muon_norm_kernel, dim3(unsigned(batch)),
                dim3(256), s, static_cast<const float*>(part), p.prep_tiles, eps, inv);
     if (e != hipSuccess) return int(e);
+    // scale: read X; write X, XT (2 + 2 + 2 bytes per padded element)
+    e = launch(K_MUON_SCALE, 0, 0.0, 6.0 * B * double(p.mp) * double(p.np), muon_scale_kernel, pgrid, dim3(256), s,
+               pa, static_cast<const float*>(inv));
+    if (e != hipSuccess) return int(e);
 
     if (ns_steps == 0) {
         return int(launch(K_MUON_APPLY0, 0, 0.0, 10.0 * B * m * n, muon_apply0_kernel, dim3(1024, unsigned(batch)),
-                          dim3(256), s, descs, pa, static_cast<const float*>(inv), keep));
+                          dim3(256), s, descs, pa, keep));
     }
     const double f_gram = B * m * m * n, f_poly = B * m * m * m, f_upd = 2.0 * B * m * m * n;
     int cur = 0;
     for (int it = 0; it < ns_steps; ++it) {
-        const bool first = (it == 0), last = (it == ns_steps - 1);
-        GemmArgs gg = gram_args(X, A, p.mp, p.np, p.tile);
-        gg.inv = inv;
-        e = first ? launch_gemm<MODE_GRAM, true>(p.tile, gg, descs, batch, f_gram, s)
-                  : launch_gemm<MODE_GRAM, false>(p.tile, gg, descs, batch, f_gram, s);
+        const bool last = (it == ns_steps - 1);
+        e = launch_gemm<MODE_GRAM>(p.tile, gram_args(X, A, p.mp, p.np, p.tile), descs, batch, f_gram, s);
         if (e != hipSuccess) return int(e);
-        GemmArgs gp = poly_args(A, Bm, p.mp, p.tile, b, c);
-        e = launch_gemm<MODE_POLY, false>(p.tile, gp, descs, batch, f_poly, s);
+        e = launch_gemm<MODE_POLY>(p.tile, poly_args(A, Bm, p.mp, p.tile, b, c), descs, batch, f_poly, s);
         if (e != hipSuccess) return int(e);
         GemmArgs gu = update_args(Bm, XT[cur], X, last ? nullptr : XT[cur ^ 1], p.mp, p.np, p.tile, a);
-        gu.inv = inv;
         if (last) {
             gu.keep = keep;
             gu.m = p.m;
             gu.n = p.n;
-            e = first ? launch_gemm<MODE_APPLY, true>(p.tile, gu, descs, batch, f_upd, s)
-                      : launch_gemm<MODE_APPLY, false>(p.tile, gu, descs, batch, f_upd, s);
+            e = launch_gemm<MODE_APPLY>(p.tile, gu, descs, batch, f_upd, s);
         } else {
-            e = first ? launch_gemm<MODE_UPDATE, true>(p.tile, gu, descs, batch, f_upd, s)
-                      : launch_gemm<MODE_UPDATE, false>(p.tile, gu, descs, batch, f_upd, s);
+            e = launch_gemm<MODE_UPDATE>(p.tile, gu, descs, batch, f_upd, s);
         }
         if (e != hipSuccess) return int(e);
         cur ^= 1;
@@ -582,10 +634,10 @@ extern "C" int mamw_ns_gram(const uint16_t* X, uint16_t* A, int batch, int64_t m
     if (!X || !A) return MAMW_ERR_NULL;
     if (!al16(X) || !al16(A)) return MAMW_ERR_ALIGN;
     const int tile = (m % 256 == 0) ? choose_tile(m, batch) : 128;
-    GemmArgs g = gram_args(X, A, m, k, tile);
     MuonBatchDescs d{};
-    return int(launch_gemm<MODE_GRAM, false>(tile, g, d, batch, double(batch) * double(m) * double(m) * double(k),
-                                             static_cast<hipStream_t>(stream)));
+    return int(launch_gemm<MODE_GRAM>(tile, gram_args(X, A, m, k, tile), d, batch,
+                                      double(batch) * double(m) * double(m) * double(k),
+                                      static_cast<hipStream_t>(stream)));
 }
 
 extern "C" int mamw_ns_poly(const uint16_t* A, uint16_t* B, int batch, int64_t m, float b, float c,
@@ -596,10 +648,10 @@ extern "C" int mamw_ns_poly(const uint16_t* A, uint16_t* B, int batch, int64_t m
     if (!al16(A) || !al16(B)) return MAMW_ERR_ALIGN;
     if (A == B) return MAMW_ERR_ALIAS;
     const int tile = (m % 256 == 0) ? choose_tile(m, batch) : 128;
-    GemmArgs g = poly_args(A, B, m, tile, b, c);
     MuonBatchDescs d{};
-    return int(launch_gemm<MODE_POLY, false>(tile, g, d, batch, double(batch) * double(m) * double(m) * double(m),
-                                             static_cast<hipStream_t>(stream)));
+    return int(launch_gemm<MODE_POLY>(tile, poly_args(A, B, m, tile, b, c), d, batch,
+                                      double(batch) * double(m) * double(m) * double(m),
+                                      static_cast<hipStream_t>(stream)));
 }
 
 extern "C" int mamw_ns_update(const uint16_t* B, const uint16_t* X, const uint16_t* XT, uint16_t* out,
@@ -613,11 +665,10 @@ extern "C" int mamw_ns_update(const uint16_t* B, const uint16_t* X, const uint16
     if (out_t && (out_t == XT)) return MAMW_ERR_ALIAS;
     (void)X;  // X enters through its transpose XT (operand and epilogue source)
     const int tile = (m % 256 == 0 && n % 256 == 0) ? choose_tile(m, batch) : 128;
-    GemmArgs g = update_args(B, XT, out, out_t, m, n, tile, a);
     MuonBatchDescs d{};
-    return int(launch_gemm<MODE_UPDATE, false>(tile, g, d, batch,
-                                               2.0 * double(batch) * double(m) * double(m) * double(n),
-                                               static_cast<hipStream_t>(stream)));
+    return int(launch_gemm<MODE_UPDATE>(tile, update_args(B, XT, out, out_t, m, n, tile, a), d, batch,
+                                        2.0 * double(batch) * double(m) * double(m) * double(n),
+                                        static_cast<hipStream_t>(stream)));
 }
 
 extern "C" int mamw_transpose_bf16(const uint16_t* src, uint16_t* dst, int batch, int64_t rows,
