@@ -26,7 +26,6 @@ constexpr int kBK = 64;
 enum GemmMode { MODE_GRAM = 0, MODE_POLY = 1, MODE_UPDATE = 2, MODE_APPLY = 3 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
-typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 
 // ---------------------------------------------------------------------------
 // Prep: one 64 x 64 tile of X (in X coordinates) per block.
@@ -196,12 +195,18 @@ __global__ __launch_bounds__(256) void muon_apply0_kernel(const MuonBatchDescs d
 // Block tile BM x BM, 4 waves in a 2 x 2 layout, each wave a (BM/2) x (BM/2)
 // sub-tile built from v_mfma_f32_32x32x16_bf16 (accumulators in AGPRs).  K
 // advances in steps of 64 through two LDS buffers filled straight from global
-// memory by global_load_lds_dwordx4 (no VGPR staging): the loads of step k+1
-// are issued right after the barrier that opens step k and land while step k's
-// MFMAs run.  Within a step, the fragments of the next 16-wide slice are read
-// while the current slice's MFMAs run.  LDS rows are 128 bytes with the
-// 16-byte chunk index XOR-swizzled (lds_chunk), so fragment reads are
-// bank-conflict free.
+// memory by buffer_load_dwordx4 ... lds (no VGPR staging; one buffer resource
+// per operand tile, so a lane needs a single 32-bit offset per operand).
+//
+// A step is four 16-wide k slices of NMF MFMAs each.  Every slice issues its
+// MFMAs one at a time with the next slice's fragment reads, and in the last
+// slice the DMA of the step after next, woven in between (sched_barrier keeps
+// that order), so the matrix pipe never waits for an address computation or a
+// burst of loads.  The block barrier sits before the last slice: the MFMAs of
+// that slice run from registers while the barrier releases the buffer just
+// read, and the next step's first fragments are read under them.  LDS rows
+// are 128 bytes with the 16-byte chunk index XOR-swizzled (lds_chunk), so
+// fragment reads are bank-conflict free.
 
 struct GemmArgs {
     const uint16_t* aop;  // A operand, batch 0 (rows i)
@@ -223,35 +228,56 @@ struct GemmArgs {
     int64_t m, n;         // APPLY: valid extent of X
 };
 
-// Launch block -> (matrix, tile row, tile col).  Blocks are dealt to the 8 XCDs
-// round-robin in dispatch order; the remap hands each XCD one contiguous range
-// of logical tiles (matrix-major), so the operand rows its workgroups share
-// stay in that XCD's L2.  Within a matrix, non-symmetric tiles run in groups of
-// kGroupM tile rows, column by column; symmetric ones row by row over the upper
-// triangle.
+// Launch block -> (matrix, tile row, tile col).
+//
+// The operand bytes a block needs per k step are fixed by the tile, so what
+// sets the speed is where they come from.  Blocks are dealt to the 8 XCDs
+// round-robin, 32 CUs each.  The remap gives every XCD, in each round of
+// 8 x 32 blocks, 32 consecutive logical tiles (a compact patch of one matrix
+// whose tiles share operand rows in that XCD's L2), and gives the 8 XCDs
+// neighbouring patches, so the round's operands are one matrix's worth and stay
+// in the memory-side cache.  Blocks of an incomplete last round keep their
+// index.  Logical order within a matrix: groups of kGroupM tile rows, column
+// by column (symmetric products: only the tiles with ti <= tj).
 constexpr int kXcds = 8;
+constexpr int kXcdSlots = 32;
 constexpr int kGroupM = 4;
 
 template <bool SYM>
 __device__ __forceinline__ void decode_tile(const GemmArgs& g, int& bat, int& ti, int& tj) {
     const int L = blockIdx.x, total = gridDim.x;
-    const int q = total / kXcds, r = total % kXcds;
+    const int full = (total / (kXcds * kXcdSlots)) * (kXcds * kXcdSlots);
     const int xcd = L % kXcds, j = L / kXcds;
-    const int logical = xcd < r ? xcd * (q + 1) + j : r * (q + 1) + (xcd - r) * q + j;
+    const int logical = L < full ? ((j / kXcdSlots) * kXcds + xcd) * kXcdSlots + j % kXcdSlots : L;
     bat = logical / g.tiles_per_matrix;
     int t = logical - bat * g.tiles_per_matrix;
+    const int T = g.tiles_m;
     if (SYM) {
-        const int T = g.tiles_m;
-        ti = 0;
-        while (t >= T - ti) {
-            t -= T - ti;
-            ++ti;
+        // Group of rows [first, first+gs): a triangle (column first+c holds
+        // rows first..first+c), then full columns of gs rows.
+        int first = 0, gs = min(kGroupM, T);
+        for (;;) {
+            const int gtiles = gs * (gs + 1) / 2 + (T - first - gs) * gs;
+            if (t < gtiles) break;
+            t -= gtiles;
+            first += gs;
+            gs = min(kGroupM, T - first);
         }
-        tj = ti + t;
+        const int tri = gs * (gs + 1) / 2;
+        if (t < tri) {
+            int c = 0;
+            while ((c + 1) * (c + 2) / 2 <= t) ++c;
+            tj = first + c;
+            ti = first + t - c * (c + 1) / 2;
+        } else {
+            t -= tri;
+            tj = first + gs + t / gs;
+            ti = first + t % gs;
+        }
     } else {
         const int width = kGroupM * g.tiles_n;
         const int group = t / width, first = group * kGroupM;
-        const int gsize = min(g.tiles_m - first, kGroupM);
+        const int gsize = min(T - first, kGroupM);
         const int w = t - group * width;
         ti = first + w % gsize;
         tj = w / gsize;
@@ -263,48 +289,67 @@ __device__ __forceinline__ void decode_tile(const GemmArgs& g, int& bat, int& ti
 // consecutive rows at one logical chunk land on 16 distinct 16-byte bank groups.
 __device__ __forceinline__ int lds_chunk(int row, int ch) { return ch ^ (row & 7) ^ ((row >> 3) & 1); }
 
+// Buffer resource over `bytes` bytes from `base` (raw buffer, 32-bit dwords).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, int(bytes), 0x00020000);
+}
+
 template <int BM, int MODE>
 __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs g, const MuonBatchDescs descs) {
     constexpr int BN = BM;
-    constexpr int WT = BM / 2;          // wave tile edge
-    constexpr int F = WT / 32;          // 32x32 fragments per wave edge
-    constexpr int LOADS = BM / 32;      // global_load_lds per wave per operand per step (8 rows each)
+    constexpr int WT = BM / 2;              // wave tile edge
+    constexpr int F = WT / 32;              // 32x32 fragments per wave edge
+    constexpr int NMF = F * F;              // MFMAs per 16-wide k slice
+    constexpr int LOADS = BM / 32;          // DMA loads per wave per operand per step (8 rows each)
+    constexpr int RPM = (2 * F + NMF - 1) / NMF;      // fragment reads woven in per MFMA
+    constexpr int LPM = (2 * LOADS + NMF - 1) / NMF;  // DMA loads woven in per MFMA
     constexpr int STAGE = (BM + BN) * kBK;  // bf16 elements per LDS stage
     constexpr bool SYM = (MODE == MODE_GRAM || MODE == MODE_POLY);
     __shared__ uint4 smem_v[2 * STAGE / 8];
     uint16_t* smem = reinterpret_cast<uint16_t*>(smem_v);
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     int bat, ti, tj;
     decode_tile<SYM>(g, bat, ti, tj);
     const uint16_t* Ag = g.aop + bat * g.a_bs + int64_t(ti) * BM * g.lda;
     const uint16_t* Bg = g.bop + bat * g.b_bs + int64_t(tj) * BN * g.ldb;
+    // The tile's rows of each operand, up to column K of its last row.
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(Ag, ((BM - 1) * g.lda + g.K) * 2);
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bg, ((BN - 1) * g.ldb + g.K) * 2);
 
-    // Wave w fills rows [w*BM/4, (w+1)*BM/4) of each operand tile, 8 rows (1 KB)
-    // per instruction: lane l lands at physical chunk l&7 of row l>>3, so it
-    // fetches the logical chunk stored there.
+    // Load i (0..LOADS-1) of an operand fills rows row0 = wave*BM/4 + 8i ..
+    // row0+7: lane l lands at physical chunk l&7 of row row0 + l/8, which holds
+    // logical chunk (l&7) ^ (l/8) ^ (i&1)  (lds_chunk with row0 a multiple of 8).
     const int lrow = lane >> 3;
-    auto issue = [&](int k0, int buf) {
-        uint16_t* As = smem + buf * STAGE;
-        uint16_t* Bs = As + BM * kBK;
-#pragma unroll
-        for (int i = 0; i < LOADS; ++i) {
-            const int row0 = wave * (BM / 4) + i * 8, row = row0 + lrow;
-            const int ch = lds_chunk(row, lane & 7);
-            __builtin_amdgcn_global_load_lds((gbl_ptr_t)(Ag + row * g.lda + k0 + ch * 8), (lds_ptr_t)(As + row0 * kBK),
-                                             16, 0, 0);
-            __builtin_amdgcn_global_load_lds((gbl_ptr_t)(Bg + row * g.ldb + k0 + ch * 8), (lds_ptr_t)(Bs + row0 * kBK),
-                                             16, 0, 0);
-        }
+    const int lda2 = int(g.lda) * 2, ldb2 = int(g.ldb) * 2;
+    const int va0 = lrow * lda2 + (((lane & 7) ^ lrow) << 4), va1 = lrow * lda2 + (((lane & 7) ^ lrow ^ 1) << 4);
+    const int vb0 = lrow * ldb2 + (((lane & 7) ^ lrow) << 4), vb1 = lrow * ldb2 + (((lane & 7) ^ lrow ^ 1) << 4);
+    // DMA number i: operand A for i < LOADS, else B.
+    auto load1 = [&](int i, int k0, int buf) {
+        const int ii = i % LOADS, row0 = wave * (BM / 4) + ii * 8;
+        uint16_t* dst = smem + buf * STAGE + (i < LOADS ? 0 : BM * kBK) + row0 * kBK;
+        if (i < LOADS)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)dst, 16, (ii & 1) ? va1 : va0,
+                                                     row0 * lda2 + k0 * 2, 0, 0);
+        else
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)dst, 16, (ii & 1) ? vb1 : vb0,
+                                                     row0 * ldb2 + k0 * 2, 0, 0);
     };
-    auto frags = [&](bf16x8_t (&fa)[F], bf16x8_t (&fb)[F], const uint16_t* As, const uint16_t* Bs, int ks) {
+    // Fragment read j of slice ks, in the order the MFMAs first use them
+    // (a-major): fa0, fb0 .. fb[F-1], fa1 .. fa[F-1].
+    auto read1 = [&](bf16x8_t (&fa)[F], bf16x8_t (&fb)[F], int buf, int ks, int j) {
+        const uint16_t* base = smem + buf * STAGE;
         const int ch = ks * 2 + (lane >> 5);
-#pragma unroll
-        for (int f = 0; f < F; ++f) {
-            const int ra = wm * WT + f * 32 + (lane & 31), rb = wn * WT + f * 32 + (lane & 31);
-            fa[f] = *reinterpret_cast<const bf16x8_t*>(As + ra * kBK + (lds_chunk(ra, ch) << 3));
-            fb[f] = *reinterpret_cast<const bf16x8_t*>(Bs + rb * kBK + (lds_chunk(rb, ch) << 3));
+        const bool isa = (j == 0) || (j > F);
+        const int f = j == 0 ? 0 : (j <= F ? j - 1 : j - F);
+        if (isa) {
+            const int r = wm * WT + f * 32 + (lane & 31);
+            fa[f] = *reinterpret_cast<const bf16x8_t*>(base + r * kBK + (lds_chunk(r, ch) << 3));
+        } else {
+            const int r = wn * WT + f * 32 + (lane & 31);
+            fb[f] = *reinterpret_cast<const bf16x8_t*>(base + BM * kBK + r * kBK + (lds_chunk(r, ch) << 3));
         }
     };
 
@@ -315,35 +360,58 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         for (int b = 0; b < F; ++b)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
-    auto mfmas = [&](const bf16x8_t (&fa)[F], const bf16x8_t (&fb)[F]) {
+    // One slice: MFMAs on (ca, cb); reads of the next slice into (na, nb) when
+    // `reads`; the DMA of step k0/kBK into buffer lbuf when `loads`.  All flags
+    // are compile-time constants at every call, so the body has no branches.
+    auto slice = [&](const bf16x8_t (&ca)[F], const bf16x8_t (&cb)[F], bf16x8_t (&na)[F], bf16x8_t (&nb)[F],
+                     bool reads, int rbuf, int rks, bool loads, int k0, int lbuf) {
 #pragma unroll
-        for (int a = 0; a < F; ++a)
+        for (int i = 0; i < NMF; ++i) {
+            acc[i / F][i % F] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[i / F], cb[i % F], acc[i / F][i % F], 0, 0, 0);
 #pragma unroll
-            for (int b = 0; b < F; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+            for (int r = 0; r < RPM; ++r)
+                if (reads && i * RPM + r < 2 * F) read1(na, nb, rbuf, rks, i * RPM + r);
+#pragma unroll
+            for (int l = 0; l < LPM; ++l)
+                if (loads && i * LPM + l < 2 * LOADS) load1(i * LPM + l, k0, lbuf);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
 
     const int KT = g.K / kBK;
-    issue(0, 0);
-    for (int kt = 0; kt < KT; ++kt) {
-        const int buf = kt & 1;
-        // Step kt's loads (own) have landed; after the barrier every wave's have,
-        // and every wave is done reading the other buffer (step kt-1).
-        __builtin_amdgcn_s_waitcnt(0x3f70);  // vmcnt(0)
-        __syncthreads();
-        if (kt + 1 < KT) issue((kt + 1) * kBK, buf ^ 1);
-        const uint16_t* As = smem + buf * STAGE;
-        const uint16_t* Bs = As + BM * kBK;
-        bf16x8_t fa0[F], fb0[F], fa1[F], fb1[F];
-        frags(fa0, fb0, As, Bs, 0);
-        frags(fa1, fb1, As, Bs, 1);
-        mfmas(fa0, fb0);
-        frags(fa0, fb0, As, Bs, 2);
-        mfmas(fa1, fb1);
-        frags(fa1, fb1, As, Bs, 3);
-        mfmas(fa0, fb0);
-        mfmas(fa1, fb1);
+#pragma unroll
+    for (int i = 0; i < 2 * LOADS; ++i) load1(i, 0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    if (KT > 1) {
+#pragma unroll
+        for (int i = 0; i < 2 * LOADS; ++i) load1(i, kBK, 1);
     }
+    bf16x8_t fa0[F], fb0[F], fa1[F], fb1[F];
+#pragma unroll
+    for (int j = 0; j < 2 * F; ++j) read1(fa0, fb0, 0, 0, j);
+    // Steps 0..KT-2.  Before the barrier this wave's loads of step kt+1 and its
+    // reads of the last slice are complete; after it everyone's are, so buffer
+    // `buf` takes step kt+2 (the last step again when kt+2 == KT, into a buffer
+    // nothing reads any more, which keeps the loop free of branches).
+    for (int kt = 0; kt < KT - 1; ++kt) {
+        const int buf = kt & 1;
+        slice(fa0, fb0, fa1, fb1, true, buf, 1, false, 0, 0);
+        slice(fa1, fb1, fa0, fb0, true, buf, 2, false, 0, 0);
+        slice(fa0, fb0, fa1, fb1, true, buf, 3, false, 0, 0);
+        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+        asm volatile("s_barrier" ::: "memory");
+        slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, true, min(kt + 2, KT - 1) * kBK, buf);
+    }
+    {
+        const int buf = (KT - 1) & 1;
+        slice(fa0, fb0, fa1, fb1, true, buf, 1, false, 0, 0);
+        slice(fa1, fb1, fa0, fb0, true, buf, 2, false, 0, 0);
+        slice(fa0, fb0, fa1, fb1, true, buf, 3, false, 0, 0);
+        slice(fa1, fb1, fa0, fb0, false, 0, 0, false, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070);  // no DMA outlives the loop
 
     // Epilogue.  Lane holds, for fragment (a,b) and register group q (0..3),
     // rows rbase..rbase+3 of column col.
