@@ -294,6 +294,47 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, int(bytes), 0x00020000);
 }
 
+// APPLY on up to 8 consecutive elements of one parameter row: with u the bf16
+// update values in w, param[prow][pcol+e] = param*keep - slr*u (and upd = u)
+// for e < min(cap, left).
+__device__ __forceinline__ void apply_chunk(const MuonMatDesc& d, uint4 w, int64_t prow, int64_t pcol, int64_t cap,
+                                            int64_t left, float keep) {
+    const int64_t nv = cap < left ? cap : left;
+    if (nv <= 0) return;
+    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    float u[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        u[2 * j] = bf16_to_f32(ww[j] & 0xffffu);
+        u[2 * j + 1] = bf16_to_f32(ww[j] >> 16);
+    }
+    const int64_t idx = prow * d.cols + pcol;
+    float* p = d.param + idx;
+    float* up = d.upd ? d.upd + idx : nullptr;
+    if (nv == 8 && ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(up)) & 15) == 0) {
+        float4 p0 = reinterpret_cast<const float4*>(p)[0], p1 = reinterpret_cast<const float4*>(p)[1];
+        p0.x = __builtin_fmaf(-d.slr, u[0], p0.x * keep);
+        p0.y = __builtin_fmaf(-d.slr, u[1], p0.y * keep);
+        p0.z = __builtin_fmaf(-d.slr, u[2], p0.z * keep);
+        p0.w = __builtin_fmaf(-d.slr, u[3], p0.w * keep);
+        p1.x = __builtin_fmaf(-d.slr, u[4], p1.x * keep);
+        p1.y = __builtin_fmaf(-d.slr, u[5], p1.y * keep);
+        p1.z = __builtin_fmaf(-d.slr, u[6], p1.z * keep);
+        p1.w = __builtin_fmaf(-d.slr, u[7], p1.w * keep);
+        reinterpret_cast<float4*>(p)[0] = p0;
+        reinterpret_cast<float4*>(p)[1] = p1;
+        if (up) {
+            reinterpret_cast<float4*>(up)[0] = make_float4(u[0], u[1], u[2], u[3]);
+            reinterpret_cast<float4*>(up)[1] = make_float4(u[4], u[5], u[6], u[7]);
+        }
+    } else {
+        for (int e = 0; e < nv; ++e) {
+            p[e] = __builtin_fmaf(-d.slr, u[e], p[e] * keep);
+            if (up) up[e] = u[e];
+        }
+    }
+}
+
 template <int BM, int MODE>
 __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs g, const MuonBatchDescs descs) {
     constexpr int BN = BM;
@@ -413,81 +454,118 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     }
     __builtin_amdgcn_s_waitcnt(0x0070);  // no DMA outlives the loop
 
-    // Epilogue.  Lane holds, for fragment (a,b) and register group q (0..3),
-    // rows rbase..rbase+3 of column col.
+    // Epilogue, staged through LDS so that every global access is a 16-byte
+    // piece of a contiguous row segment.  TT holds the tile transposed: TT row x
+    // (tile column) holds the BM tile rows y in 16-byte chunks, logical chunk c
+    // at physical chunk c ^ (x ^ x>>3) (mod chunks per row).  That spreads both
+    // a lane's 4 rows of one column and 8 columns gathered at one row over the
+    // banks (at most 2-way).
+    constexpr int NCH = BM / 8;  // 16-byte chunks per TT row
+    uint16_t* const TT = smem;   // BN rows x BM bf16 (fits in the two stages)
+    auto tt = [&](int x, int y) { return x * BM + ((((y >> 3) ^ x ^ (x >> 3)) & (NCH - 1)) << 3) + (y & 7); };
+    const bool diag = SYM && ti == tj;
+    __syncthreads();  // every wave is done with the stage buffers
+
+    if constexpr (MODE != MODE_GRAM) {
+        // Coefficient operand, TT[x][y] = src[(tj*BN + x) * lds + ti*BM + y]:
+        // A is symmetric (A[r][col] = A[col][r]); X^T holds X transposed.
+        const uint16_t* S = g.src + bat * g.src_bs + int64_t(tj) * BN * g.lds + int64_t(ti) * BM;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(S, ((BN - 1) * g.lds + BM) * 2);
+        constexpr int RPI = 64 / NCH;        // TT rows per 1-KB load
+        constexpr int NLD = BN / RPI / 4;    // loads per wave
+        const int lds2 = int(g.lds) * 2;
+        for (int i = 0; i < NLD; ++i) {
+            const int x0 = (wave * NLD + i) * RPI, x = x0 + lane / NCH;
+            const int c = ((lane % NCH) ^ x ^ (x >> 3)) & (NCH - 1);  // logical chunk at physical lane % NCH
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(TT + x0 * BM), 16, (lane / NCH) * lds2 + c * 16,
+                                                     x0 * lds2, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+        __syncthreads();
+    }
+
+    // Lane holds, for fragment (a,b) and register group q, rows y..y+3 of
+    // column x: one 8-byte TT cell, combined with src in place.
 #pragma unroll
     for (int a = 0; a < F; ++a) {
 #pragma unroll
         for (int b = 0; b < F; ++b) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int64_t rbase = int64_t(ti) * BM + wm * WT + a * 32 + q * 8 + (lane >> 5) * 4;
-                const int64_t col = int64_t(tj) * BN + wn * WT + b * 32 + (lane & 31);
+                const int y = wm * WT + a * 32 + q * 8 + (lane >> 5) * 4;
+                const int x = wn * WT + b * 32 + (lane & 31);
+                uint2* cell = reinterpret_cast<uint2*>(TT + tt(x, y));
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = acc[a][b][q * 4 + e];
-                if (MODE == MODE_GRAM || MODE == MODE_POLY) {
-                    if (MODE == MODE_POLY) {
-                        // A is exactly symmetric: A[r][col] = A[col][r], one 8-byte load.
-                        const uint2 s2 = *reinterpret_cast<const uint2*>(g.src + bat * g.src_bs + col * g.lds + rbase);
-                        const float s[4] = {bf16_to_f32(s2.x & 0xffffu), bf16_to_f32(s2.x >> 16),
-                                            bf16_to_f32(s2.y & 0xffffu), bf16_to_f32(s2.y >> 16)};
+                if constexpr (MODE != MODE_GRAM) {
+                    const uint2 s2 = *cell;
+                    const float sv[4] = {bf16_to_f32(s2.x & 0xffffu), bf16_to_f32(s2.x >> 16),
+                                         bf16_to_f32(s2.y & 0xffffu), bf16_to_f32(s2.y >> 16)};
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) v[e] = __builtin_fmaf(g.alpha, v[e], g.beta * s[e]);
-                    }
-                    uint32_t h[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) h[e] = f32_to_bf16(v[e]);
-                    uint16_t* C = g.c + bat * g.c_bs;
-                    if (ti != tj) {
-                        uint2 pk;
-                        pk.x = h[0] | (h[1] << 16);
-                        pk.y = h[2] | (h[3] << 16);
-                        *reinterpret_cast<uint2*>(C + col * g.ldc + rbase) = pk;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) C[(rbase + e) * g.ldc + col] = uint16_t(h[e]);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            if (rbase + e <= col) {
-                                C[(rbase + e) * g.ldc + col] = uint16_t(h[e]);
-                                C[col * g.ldc + rbase + e] = uint16_t(h[e]);
-                            }
-                        }
-                    }
-                } else {
-                    // X[r][col] = XT[col][r]: read 4 consecutive rows with one 8-byte load.
-                    const uint2 s2 = *reinterpret_cast<const uint2*>(g.src + bat * g.src_bs + col * g.lds + rbase);
-                    const uint32_t xs[4] = {s2.x & 0xffffu, s2.x >> 16, s2.y & 0xffffu, s2.y >> 16};
-                    uint32_t h[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) h[e] = f32_to_bf16(__builtin_fmaf(g.beta, bf16_to_f32(xs[e]), v[e]));
-                    if (MODE == MODE_UPDATE) {
-                        uint16_t* C = g.c + bat * g.c_bs;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) C[(rbase + e) * g.ldc + col] = uint16_t(h[e]);
-                        if (g.ct) {
-                            uint2 pk;
-                            pk.x = h[0] | (h[1] << 16);
-                            pk.y = h[2] | (h[3] << 16);
-                            *reinterpret_cast<uint2*>(g.ct + bat * g.ct_bs + col * g.ldct + rbase) = pk;
-                        }
-                    } else {  // MODE_APPLY
-                        const MuonMatDesc& d = descs.d[bat];
-                        if (col < g.n) {
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                const int64_t r = rbase + e;
-                                if (r < g.m) {
-                                    const int64_t idx = d.tall ? col * d.cols + r : r * d.cols + col;
-                                    const float u = bf16_to_f32(h[e]);
-                                    d.param[idx] = __builtin_fmaf(-d.slr, u, d.param[idx] * g.keep);
-                                    if (d.upd) d.upd[idx] = u;
-                                }
-                            }
-                        }
-                    }
+                    for (int e = 0; e < 4; ++e)
+                        v[e] = MODE == MODE_POLY ? __builtin_fmaf(g.alpha, v[e], g.beta * sv[e])
+                                                 : __builtin_fmaf(g.beta, sv[e], v[e]);
                 }
+                uint32_t h[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) h[e] = f32_to_bf16(v[e]);
+                *cell = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+            }
+        }
+    }
+    __syncthreads();
+    if (diag) {
+        // Diagonal tile of a symmetric product: the upper triangle (y <= x) is
+        // authoritative; each lower element takes its mirror, so the output is
+        // exactly symmetric.  Reads touch only upper cells, writes only lower.
+        for (int k = tid; k < BM * NCH; k += kGemmThreads) {
+            const int y = k / NCH, xc = (k % NCH) * 8;
+            if (xc >= y) continue;
+            const uint4 w = *reinterpret_cast<const uint4*>(TT + tt(y, xc));  // elements (xc..xc+7, y)
+            const uint16_t* hv = reinterpret_cast<const uint16_t*>(&w);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (xc + j < y) TT[tt(xc + j, y)] = hv[j];
+        }
+        __syncthreads();
+    }
+
+    // Transposed orientation, from TT rows: row (tj*BN + x) of the output holds
+    // TT row x.  Symmetric products: the mirror block (the tile itself on the
+    // diagonal); UPDATE: X^T; APPLY: the parameter of a tall matrix.
+    const MuonMatDesc& d = descs.d[bat];
+    const bool tall = MODE == MODE_APPLY && d.tall;
+    if (SYM || (MODE == MODE_UPDATE && g.ct) || tall) {
+        for (int k = tid; k < BN * NCH; k += kGemmThreads) {
+            const int x = k / NCH, c = k % NCH;
+            const uint4 w = *reinterpret_cast<const uint4*>(TT + x * BM + (((c ^ x ^ (x >> 3)) & (NCH - 1)) << 3));
+            const int64_t orow = int64_t(tj) * BN + x, ocol = int64_t(ti) * BM + c * 8;
+            if constexpr (MODE == MODE_APPLY) {
+                apply_chunk(d, w, orow, ocol, orow < g.n ? int64_t(8) : int64_t(0), g.m - ocol, g.keep);
+            } else if constexpr (SYM) {
+                *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + orow * g.ldc + ocol) = w;
+            } else {
+                *reinterpret_cast<uint4*>(g.ct + bat * g.ct_bs + orow * g.ldct + ocol) = w;
+            }
+        }
+    }
+    // Direct orientation, gathered from TT columns: row (ti*BM + y) of the
+    // output holds TT[x][y] over x.  Symmetric products: the tile's own block
+    // (off the diagonal); UPDATE: X; APPLY: the parameter of a wide matrix.
+    if ((SYM && !diag) || MODE == MODE_UPDATE || (MODE == MODE_APPLY && !tall)) {
+        for (int k = tid; k < BM * (BN / 8); k += kGemmThreads) {
+            const int y = k / (BN / 8), xc = (k % (BN / 8)) * 8;
+            uint32_t w[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                w[j] = uint32_t(TT[tt(xc + 2 * j, y)]) | (uint32_t(TT[tt(xc + 2 * j + 1, y)]) << 16);
+            const uint4 wv = make_uint4(w[0], w[1], w[2], w[3]);
+            const int64_t orow = int64_t(ti) * BM + y, ocol = int64_t(tj) * BN + xc;
+            if constexpr (MODE == MODE_APPLY) {
+                apply_chunk(d, wv, orow, ocol, orow < g.m ? int64_t(8) : int64_t(0), g.n - ocol, g.keep);
+            } else {
+                *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + orow * g.ldc + ocol) = wv;
             }
         }
     }
