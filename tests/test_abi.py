@@ -68,11 +68,11 @@ def _pack(tensors):
 def test_adamw_pack_blocks_and_records():
     st, buf, blocks = _pack([_t(1 << 40, 4096), _t(2 << 40, 1), _t(3 << 40, 0), _t(4 << 40, 10000)])
     assert st == OK
-    assert blocks == 1 + 1 + 0 + 3  # 4096-element chunks
+    assert blocks == 4 + 1 + 0 + 10  # 1024-element chunks
     import struct
 
     begins = [struct.unpack_from("<q", buf, 64 * i + 40)[0] for i in range(4)]
-    assert begins == [0, 1, 2, 2]
+    assert begins == [0, 4, 5, 5]
     vec_ok = [struct.unpack_from("<i", buf, 64 * i + 48)[0] for i in range(4)]
     assert vec_ok == [1, 1, 1, 1]
     st, buf, _ = _pack([_t((1 << 40) + 4, 100)])  # 4-byte aligned, not 16

@@ -1,8 +1,9 @@
 // AdamW update for gfx950: one single-pass kernel over every tensor of a step.
 //
-// Each 256-thread block owns one 4096-element chunk of one tensor and moves it
-// with 16-byte (dwordx4) loads and stores: 16 loads in flight per thread, then
-// the update, then 12 stores.  HBM traffic is the algorithmic minimum, 28 bytes
+// Each 256-thread block owns one 1024-element chunk of one tensor and moves it
+// with non-temporal 16-byte (dwordx4) loads and stores: 4 loads per thread,
+// the update, 3 stores.  Small chunks keep many short-lived waves in flight
+// per CU, which measured faster than fewer, longer ones.  HBM traffic is the algorithmic minimum, 28 bytes
 // per element (read p, g, m, v; write p, m, v).
 //
 // Arithmetic follows triton_adam.py:53-59 operation by operation in IEEE fp32
@@ -47,6 +48,19 @@ __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v
     v = vt;
 }
 
+// Streaming 16-byte accesses: every byte is touched once, so the loads and
+// stores are non-temporal (measured: +6-8 points of HBM bandwidth over plain
+// accesses on this kernel; either half alone gains nothing).
+typedef float nt_f4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 nt_load(const float4* q) {
+    const nt_f4 v = __builtin_nontemporal_load(reinterpret_cast<const nt_f4*>(q));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void nt_store(float4* q, float4 x) {
+    const nt_f4 v = {x.x, x.y, x.z, x.w};
+    __builtin_nontemporal_store(v, reinterpret_cast<nt_f4*>(q));
+}
+
 __device__ __forceinline__ void adamw_vec(float4& p, float4 g, float4& m, float4& v,
                                           const AdamWConsts& c) {
     adamw_elem(p.x, g.x, m.x, v.x, c);
@@ -72,18 +86,18 @@ __device__ __forceinline__ void adamw_chunk(const AdamWRec& r, int64_t start, in
 #pragma unroll
         for (int u = 0; u < kAdamWUnroll; ++u) {
             const int i = u * kAdamWThreads + tid;
-            p[u] = P4[i];
-            g[u] = G4[i];
-            m[u] = M4[i];
-            v[u] = V4[i];
+            p[u] = nt_load(P4 + i);
+            g[u] = nt_load(G4 + i);
+            m[u] = nt_load(M4 + i);
+            v[u] = nt_load(V4 + i);
         }
 #pragma unroll
         for (int u = 0; u < kAdamWUnroll; ++u) {
             const int i = u * kAdamWThreads + tid;
             adamw_vec(p[u], g[u], m[u], v[u], c);
-            P4[i] = p[u];
-            M4[i] = m[u];
-            V4[i] = v[u];
+            nt_store(P4 + i, p[u]);
+            nt_store(M4 + i, m[u]);
+            nt_store(V4 + i, v[u]);
         }
         return;
     }
@@ -95,11 +109,11 @@ __device__ __forceinline__ void adamw_chunk(const AdamWRec& r, int64_t start, in
         float4* M4 = reinterpret_cast<float4*>(M);
         float4* V4 = reinterpret_cast<float4*>(V);
         for (int i = tid; i < nv; i += kAdamWThreads) {
-            float4 p = P4[i], m = M4[i], v = V4[i];
-            adamw_vec(p, G4[i], m, v, c);
-            P4[i] = p;
-            M4[i] = m;
-            V4[i] = v;
+            float4 p = nt_load(P4 + i), m = nt_load(M4 + i), v = nt_load(V4 + i);
+            adamw_vec(p, nt_load(G4 + i), m, v, c);
+            nt_store(P4 + i, p);
+            nt_store(M4 + i, m);
+            nt_store(V4 + i, v);
         }
         scalar_from = nv << 2;
     }

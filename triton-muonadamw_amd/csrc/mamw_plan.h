@@ -21,8 +21,8 @@ namespace mamw {
 // (the block count closes the last range), and covers elements
 // [(b - block_begin) * kAdamWChunk, +kAdamWChunk) of that tensor.
 constexpr int kAdamWThreads = 256;
-constexpr int kAdamWUnroll = 4;  // float4 groups per thread per block
-constexpr int64_t kAdamWChunk = int64_t(kAdamWThreads) * 4 * kAdamWUnroll;  // 4096
+constexpr int kAdamWUnroll = 1;  // float4 groups per thread per block
+constexpr int64_t kAdamWChunk = int64_t(kAdamWThreads) * 4 * kAdamWUnroll;  // 1024
 
 struct alignas(16) AdamWRec {
     float* p;
