@@ -53,6 +53,22 @@ def kernel_label(name: str, variant: int) -> str:
     return name
 
 
+def traffic_bytes(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary (profiles/hbm_traffic_llama8b.txt, scaled by a copy kernel of known size); None if absent."""
+    path = ROOT / "profiles" / "hbm_traffic_llama8b.txt"
+    try:
+        text = path.read_text()
+    except OSError:
+        return None
+    for line in text.splitlines():
+        if line.startswith("kernel="):
+            fields = dict(kv.split("=", 1) for kv in line.split("; "))
+            if fields.get("kernel") == kernel:
+                return float(fields["bytes_per_launch"])
+    return None
+
+
 def make_params(layout, dev, seed: int):
     """Parameters (N(0,0.02)) with gradients (N(0,1e-3)), generated on the device from a seeded generator."""
     import torch
@@ -255,6 +271,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extras", action="store_true", help="only the headline Llama-8B step")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="only copy 1 GiB three times (torch copy_): the known-size kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -268,6 +287,14 @@ def main():
 
     dev = torch.device("cuda:0")
     log(f"device: {torch.cuda.get_device_name(dev)}; torch {torch.__version__}")
+    if args.calib_copy:
+        x = torch.empty(1 << 28, device=dev).normal_()
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"calib_copy_bytes_each_way": x.numel() * 4, "copies": 3}), flush=True)
+        return
     layout = llama8b_layout()
     ms, agg = bench_full_step(layout, dev, args.steps, args.warmup, args.seed, "llama8b")
     dom_name, dom = max(agg.items(), key=lambda kv: kv[1]["ms"])
@@ -278,7 +305,7 @@ def main():
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-        "traffic": None,
+        "traffic": traffic_bytes(dom_name),
         "kernel": dom_name,
         "avg_launch_ms": round(dom["ms"] / dom["launches"], 4),
         "launches": dom["launches"],
