@@ -92,10 +92,13 @@ def test_muonadamw_attributes_and_state_dict():
     assert opt.param_group["adam"] is opt.adamw.model_params
     assert opt.param_group["muon"] is opt.muon.model_params
     assert opt.muon.lr == 0.02 and opt.adamw.lr == 3e-4
-    assert opt.state_dict() is opt.param_group
+    sd = opt.state_dict()  # optimizer state, not the parameter lists (those stay in param_group)
+    assert set(sd) == {"adam", "muon"} and "state" in sd["adam"] and "state" in sd["muon"]
+    # the reference's format (parameter lists, optimizer.py:170-175) still reassigns the lists
     new = [nn.Parameter(torch.zeros(2, 2))]
     opt.load_state_dict({"muon": new})
-    assert opt.muon.model_params is new
+    assert opt.muon.model_params is new and opt.param_group["muon"] is new
+    assert opt.param_groups[1]["params"] is new
     # state shapes: fp32 moments for AdamW, parameter-shaped momentum for Muon
     for p in opt.adamw.model_params:
         assert opt.adamw.m[p].shape == p.shape and opt.adamw.m[p].dtype == torch.float32

@@ -1,0 +1,145 @@
+"""Checkpoint/resume and the torch.optim surface on the GPU.
+
+* Resume: k steps, ``state_dict()`` saved (deep copy, with the parameters);
+  a fresh optimizer over fresh copies of those parameters, loaded, takes the
+  next step bit for bit like the original.
+* Cross-load: ``PyTorchMuonAdamW`` (the reference's torch wrapper,
+  optimizer.py:178-260) runs k steps, its ``state_dict()`` goes into
+  ``MuonAdamW``, and both take the next step: AdamW within 1e-6 absolute (the
+  kernels match fused torch AdamW to that), the Muon update within the
+  reference tolerance (relative Frobenius error 1e-2 on the update).
+* An LR schedule attached to ``MuonAdamW`` gives the same parameters bit for
+  bit as the same learning rates set by hand each step, and ``step(closure)``
+  returns the closure's loss.
+"""
+
+import copy
+import math
+
+import pytest
+import torch
+
+from helpers import gpt2_layout
+from triton_muon_adamw import AdamConfig, MuonAdamW, MuonConfig, PyTorchMuonAdamW
+
+pytestmark = pytest.mark.gpu
+
+MC = MuonConfig(lr=1e-3, beta=0.95, eps=1e-7, weight_decay=0.1, coeffs=(3.4445, -4.7750, 2.0315), nesterov=True,
+                ns_steps=5)
+AC = AdamConfig(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+LAYOUT = [(n, s, b) for n, s, b in gpt2_layout(n_layer=2) if not n.startswith("wte")]
+
+
+def _params(dev, seed=0):
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    return [(n, torch.nn.Parameter(torch.empty(s, device=dev).normal_(0.0, 0.02, generator=gen)), b)
+            for n, s, b in LAYOUT]
+
+
+def _split(named):
+    return {"adam": [p for _, p, b in named if b == "adam"], "muon": [p for _, p, b in named if b == "muon"]}
+
+
+def _grads(named, dev, gen):
+    return [torch.empty(p.shape, device=dev).normal_(0.0, 1e-3, generator=gen) for _, p, _ in named]
+
+
+def _set(named, grads):
+    for (_, p, _), g in zip(named, grads):
+        p.grad = g.clone()
+
+
+def test_resume_is_bit_exact(gpu):
+    named = _params(gpu)
+    opt = MuonAdamW(_split(named), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    gen = torch.Generator(device=gpu).manual_seed(1)
+    for _ in range(2):
+        _set(named, _grads(named, gpu, gen))
+        opt.step()
+    torch.cuda.synchronize()
+    saved_params = [p.detach().clone() for _, p, _ in named]
+    saved = copy.deepcopy(opt.state_dict())
+    last = _grads(named, gpu, gen)
+    _set(named, last)
+    opt.step()
+    torch.cuda.synchronize()
+
+    fresh = [(n, torch.nn.Parameter(w.clone()), b) for (n, _, b), w in zip(named, saved_params)]
+    opt2 = MuonAdamW(_split(fresh), muon_config=MuonConfig(lr=0.5), adam_config=AdamConfig(lr=0.5),
+                     parameter_split="explicit")
+    opt2.load_state_dict(saved)
+    _set(fresh, last)
+    opt2.step()
+    torch.cuda.synchronize()
+    for (n, p, _), (_, q, _) in zip(named, fresh):
+        assert torch.equal(p.detach(), q.detach()), n
+    assert opt2.adamw.step_num == 3
+
+
+def test_torch_wrapper_state_loads_into_muonadamw(gpu):
+    theirs = _params(gpu)
+    ref = PyTorchMuonAdamW(_split(theirs), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    gen = torch.Generator(device=gpu).manual_seed(2)
+    for _ in range(2):
+        _set(theirs, _grads(theirs, gpu, gen))
+        ref.step()
+    torch.cuda.synchronize()
+    mine = [(n, torch.nn.Parameter(p.detach().clone()), b) for n, p, b in theirs]
+    opt = MuonAdamW(_split(mine), muon_config=MuonConfig(lr=0.5), adam_config=AdamConfig(lr=0.5),
+                    parameter_split="explicit")
+    opt.load_state_dict(ref.state_dict())
+    before = [p.detach().clone() for _, p, _ in mine]
+    g = _grads(mine, gpu, gen)
+    _set(mine, g)
+    _set(theirs, g)
+    opt.step()
+    ref.step()
+    torch.cuda.synchronize()
+    keep = 1 - MC.lr * MC.weight_decay
+    for (n, p, b), (_, q, _), p0 in zip(mine, theirs, before):
+        if b == "adam":
+            torch.testing.assert_close(p.detach(), q.detach(), atol=1e-6, rtol=0)
+        else:
+            adj = MC.lr * math.sqrt(max(1.0, p.shape[0] / p.shape[1]))
+            u_mine = (p0.double() * keep - p.detach().double()) / adj
+            u_ref = (p0.double() * keep - q.detach().double()) / adj
+            assert ((u_mine - u_ref).norm() / u_ref.norm()).item() <= 1e-2, n
+
+
+@pytest.mark.filterwarnings("ignore:Detected call of")
+def test_lr_schedule_matches_manual_rates(gpu):
+    a, b = _params(gpu), _params(gpu)
+    opt_a = MuonAdamW(_split(a), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    opt_b = MuonAdamW(_split(b), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    sched = torch.optim.lr_scheduler.LambdaLR(opt_a, lambda s: 0.5 ** s)
+    gen = torch.Generator(device=gpu).manual_seed(3)
+    for k in range(3):
+        g = _grads(a, gpu, gen)
+        _set(a, g)
+        _set(b, g)
+        opt_a.step()
+        sched.step()
+        opt_b.adamw.lr, opt_b.muon.lr = AC.lr * 0.5 ** k, MC.lr * 0.5 ** k
+        opt_b.param_groups[0]["lr"], opt_b.param_groups[1]["lr"] = opt_b.adamw.lr, opt_b.muon.lr
+        opt_b.step()
+    torch.cuda.synchronize()
+    for (n, p, _), (_, q, _) in zip(a, b):
+        assert torch.equal(p.detach(), q.detach()), n
+
+
+def test_step_closure_returns_loss(gpu):
+    named = _params(gpu)
+    opt = MuonAdamW(_split(named), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    w = next(p for _, p, b in named if b == "muon")
+
+    def closure():
+        opt.zero_grad(set_to_none=True)
+        loss = (w.float() ** 2).sum()
+        loss.backward()
+        return loss
+
+    before = w.detach().clone()
+    loss = opt.step(closure)
+    torch.cuda.synchronize()
+    assert torch.is_tensor(loss) and loss.item() > 0
+    assert not torch.equal(before, w.detach())  # only w has a gradient; it moved

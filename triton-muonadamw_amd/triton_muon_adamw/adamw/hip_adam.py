@@ -140,11 +140,65 @@ class HipAdamW:
                     _lib.stream_handle(plan.device))
             _lib.check(st, "mamw_adamw_mt_step")
 
-    def zero_grad(self):
-        """Resets gradients back to zero."""
+    def zero_grad(self, set_to_none: bool = False):
+        """Resets gradients back to zero (the reference's behaviour), or to None
+        with ``set_to_none=True`` (torch.optim's)."""
         for param in self.model_params:
             if param.grad is not None:
-                param.grad.zero_()
+                if set_to_none:
+                    param.grad = None
+                else:
+                    param.grad.zero_()
+
+    def state_dict(self) -> dict:
+        """Optimizer state in ``torch.optim.AdamW``'s format.
+
+        ``state[i]`` holds ``exp_avg``, ``exp_avg_sq`` and ``step`` of parameter
+        ``i`` (its position in ``model_params``); every parameter carries the
+        branch's one step counter (triton_adam.py:137).  Empty before the first
+        step, as in torch.  The state tensors are returned by reference.
+        """
+        state = {}
+        if self.step_num > 0:
+            for i, p in enumerate(self.model_params):
+                state[i] = {"step": torch.tensor(float(self.step_num)), "exp_avg": self.m[p],
+                            "exp_avg_sq": self.v[p]}
+        group = {"lr": self.lr, "betas": (self.beta1, self.beta2), "eps": self.eps,
+                 "weight_decay": self.weight_decay, "amsgrad": False, "maximize": False, "foreach": None,
+                 "capturable": False, "differentiable": False, "fused": True, "decoupled_weight_decay": True,
+                 "params": list(range(len(self.model_params)))}
+        return {"state": state, "param_groups": [group]}
+
+    def load_state_dict(self, state_dict: dict) -> None:
+        """Restore a state produced by :meth:`state_dict` or by ``torch.optim.AdamW``.
+
+        Parameters are matched by position; the moments are copied into this
+        branch's own buffers (so the launch plan stays valid).  torch keeps one
+        step per parameter, this branch one for all: differing steps raise.
+        """
+        groups = state_dict["param_groups"]
+        ids = [i for g in groups for i in g["params"]]
+        if len(ids) != len(self.model_params):
+            raise ValueError("loaded state dict contains a parameter group that doesn't match the size of "
+                             "optimizer's group")
+        hyper = {(g["lr"], tuple(g["betas"]), g["eps"], g["weight_decay"]) for g in groups}
+        if len(hyper) > 1:
+            raise ValueError("parameter groups with different hyperparameters cannot be loaded into one AdamW branch")
+        pos = {pid: k for k, pid in enumerate(ids)}
+        steps = {float(st["step"]) for st in state_dict["state"].values()}
+        if len(steps) > 1:
+            raise ValueError(f"per-parameter steps differ ({sorted(steps)}); this optimizer keeps one step counter")
+        with torch.no_grad():
+            for p in self.model_params:
+                self.m[p].zero_()
+                self.v[p].zero_()
+            for pid, st in state_dict["state"].items():
+                p = self.model_params[pos[pid]]
+                self.m[p].copy_(st["exp_avg"])
+                self.v[p].copy_(st["exp_avg_sq"])
+        self.step_num = int(steps.pop()) if steps else 0
+        lr, betas, eps, wd = hyper.pop() if hyper else (self.lr, (self.beta1, self.beta2), self.eps, self.weight_decay)
+        self.lr, self.beta1, self.beta2, self.eps, self.weight_decay = lr, betas[0], betas[1], eps, wd
 
 
 # The reference's class name, for drop-in imports.

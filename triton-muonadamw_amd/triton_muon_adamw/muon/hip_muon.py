@@ -241,6 +241,7 @@ class HipMuon:
         for param in self.model_params:
             self.momentum[param] = torch.zeros_like(param, device=param.device, dtype=param.dtype)
         self._plan_key = None
+        self._plan_lr = lr
         self._calls: list[_Call] = []
         self._ws: dict[torch.device, torch.Tensor] = {}
 
@@ -294,12 +295,18 @@ class HipMuon:
         active = [p for p in self.model_params if p.grad is not None]
         if not active:
             return
-        key = (self.lr, self.adjust_lr_fn, self.steps,
-               tuple((id(p), p.data_ptr(), p.grad.data_ptr()) for p in active))
+        key = (self.adjust_lr_fn, self.steps, tuple((id(p), p.data_ptr(), p.grad.data_ptr()) for p in active))
         if key != self._plan_key:
             self._plan_key = None
             self._build_calls(active)
             self._plan_key = key
+            self._plan_lr = self.lr
+        elif self.lr != self._plan_lr:  # a schedule moved lr: refresh the per-matrix scaled lr only
+            for call in self._calls:
+                for i in range(call.n):
+                    e = call.arr[i]
+                    e.scaled_lr = scaled_lr(self.lr, self.adjust_lr_fn, e.rows, e.cols)
+            self._plan_lr = self.lr
         lib = _lib.load()
         nest = int(bool(self.is_nesterov))
         for call in self._calls:
@@ -310,11 +317,60 @@ class HipMuon:
                                         ws.numel(), _lib.stream_handle(call.device))
             _lib.check(st, "mamw_muon_step")
 
-    def zero_grad(self):
-        """Resets gradients back to zero."""
+    def zero_grad(self, set_to_none: bool = False):
+        """Resets gradients back to zero (the reference's behaviour), or to None
+        with ``set_to_none=True`` (torch.optim's)."""
         for param in self.model_params:
             if param.grad is not None:
-                param.grad.zero_()
+                if set_to_none:
+                    param.grad = None
+                else:
+                    param.grad.zero_()
+
+    def state_dict(self) -> dict:
+        """Optimizer state in ``torch.optim.Muon``'s format: ``state[i]`` holds the
+        ``momentum_buffer`` of parameter ``i`` (its position in ``model_params``),
+        returned by reference; one param group with this branch's
+        hyperparameters (``adjust_lr_fn`` ``"original"`` written as torch's
+        ``None``)."""
+        state = {i: {"momentum_buffer": self.momentum[p]} for i, p in enumerate(self.model_params)}
+        group = {"lr": self.lr, "weight_decay": self.weight_decay, "momentum": self.beta,
+                 "nesterov": self.is_nesterov, "ns_coefficients": (self.a, self.b, self.c), "eps": self.eps,
+                 "ns_steps": self.steps,
+                 "adjust_lr_fn": None if self.adjust_lr_fn == "original" else self.adjust_lr_fn,
+                 "params": list(range(len(self.model_params)))}
+        return {"state": state, "param_groups": [group]}
+
+    def load_state_dict(self, state_dict: dict) -> None:
+        """Restore a state produced by :meth:`state_dict` or by ``torch.optim.Muon``.
+
+        Parameters are matched by position; momentum buffers are copied into
+        this branch's own (parameters without saved state restart from zero,
+        as torch's lazily created buffers do).
+        """
+        groups = state_dict["param_groups"]
+        ids = [i for g in groups for i in g["params"]]
+        if len(ids) != len(self.model_params):
+            raise ValueError("loaded state dict contains a parameter group that doesn't match the size of "
+                             "optimizer's group")
+        keys = ("lr", "weight_decay", "momentum", "nesterov", "ns_coefficients", "eps", "ns_steps", "adjust_lr_fn")
+        hyper = {tuple(tuple(g[k]) if k == "ns_coefficients" else g[k] for k in keys) for g in groups}
+        if len(hyper) > 1:
+            raise ValueError("parameter groups with different hyperparameters cannot be loaded into one Muon branch")
+        pos = {pid: k for k, pid in enumerate(ids)}
+        with torch.no_grad():
+            for p in self.model_params:
+                self.momentum[p].zero_()
+            for pid, st in state_dict["state"].items():
+                self.momentum[self.model_params[pos[pid]]].copy_(st["momentum_buffer"])
+        if hyper:
+            lr, wd, beta, nesterov, coeffs, eps, steps, adjust = hyper.pop()
+            adjust = "original" if adjust is None else adjust
+            if adjust not in _ADJUST_FNS:
+                raise AssertionError(f"Invalid adjust_lr_fn: {adjust}")
+            self.lr, self.weight_decay, self.beta, self.is_nesterov = lr, wd, beta, nesterov
+            self.a, self.b, self.c = coeffs
+            self.eps, self.steps, self.adjust_lr_fn = eps, steps, adjust
 
 
 # The reference's class name, for drop-in imports.

@@ -127,7 +127,7 @@ def split_parameters(
     return adam_params, muon_params
 
 
-class MuonAdamW(HipMuon, HipAdamW):
+class MuonAdamW(HipMuon, HipAdamW, torch.optim.Optimizer):
     """Hybrid optimizer: Muon for 2-D weight matrices, AdamW for the rest.
 
     Two-dimensional parameters are updated with Muon, except the input
@@ -152,6 +152,15 @@ class MuonAdamW(HipMuon, HipAdamW):
     -----
     The update kernels are gfx950 HIP kernels; parameters must be contiguous
     float32 tensors on a ROCm device when ``step()`` runs.
+
+    Beyond the reference's surface, the optimizer is a ``torch.optim.Optimizer``
+    with two ``param_groups`` (0: the AdamW branch, 1: the Muon branch, with
+    torch.optim.AdamW / torch.optim.Muon hyperparameter names), so LR schedulers
+    attach and hyperparameters edited there take effect at the next ``step``;
+    ``step(closure)`` re-evaluates the loss first; ``zero_grad(set_to_none)``;
+    and ``state_dict()`` carries the optimizer state (moments, step, momentum)
+    in the format of ``PyTorchMuonAdamW.state_dict()``, so checkpoints move
+    between the two in both directions.
     """
 
     def __init__(
@@ -184,27 +193,89 @@ class MuonAdamW(HipMuon, HipAdamW):
             "adam": self.adamw.model_params,
             "muon": self.muon.model_params,
         }
+        torch.optim.Optimizer.__init__(self, [self._adam_group(), self._muon_group()], {})
+        self._push_groups()  # the groups share the branches' parameter lists
 
-    def step(self) -> None:
-        """Apply one update with the AdamW branch, then the Muon branch."""
+    # -- torch.optim surface ---------------------------------------------------
+    def _adam_group(self) -> dict:
+        a = self.adamw
+        return {"params": a.model_params, "lr": a.lr, "betas": (a.beta1, a.beta2), "eps": a.eps,
+                "weight_decay": a.weight_decay, "name": "adam"}
+
+    def _muon_group(self) -> dict:
+        m = self.muon
+        return {"params": m.model_params, "lr": m.lr, "momentum": m.beta, "nesterov": m.is_nesterov,
+                "ns_coefficients": (m.a, m.b, m.c), "eps": m.eps, "ns_steps": m.steps,
+                "weight_decay": m.weight_decay, "adjust_lr_fn": m.adjust_lr_fn, "name": "muon"}
+
+    def _pull_groups(self) -> None:
+        """Hyperparameters edited in ``param_groups`` (e.g. by a scheduler) into the branches."""
+        ga, gm = self.param_groups
+        a, m = self.adamw, self.muon
+        a.lr, (a.beta1, a.beta2), a.eps, a.weight_decay = ga["lr"], ga["betas"], ga["eps"], ga["weight_decay"]
+        m.lr, m.beta, m.is_nesterov, m.eps = gm["lr"], gm["momentum"], gm["nesterov"], gm["eps"]
+        (m.a, m.b, m.c), m.steps, m.weight_decay = gm["ns_coefficients"], gm["ns_steps"], gm["weight_decay"]
+        m.adjust_lr_fn = gm["adjust_lr_fn"]
+
+    def _push_groups(self) -> None:
+        """The branches' hyperparameters (after a load) into ``param_groups``."""
+        ga, gm = self.param_groups
+        for g, new in ((ga, self._adam_group()), (gm, self._muon_group())):
+            for k, v in new.items():
+                if k != "params":
+                    g[k] = v
+        ga["params"], gm["params"] = self.adamw.model_params, self.muon.model_params
+
+    def step(self, closure=None):
+        """Apply one update with the AdamW branch, then the Muon branch.
+
+        With ``closure``, the loss is re-evaluated (under ``torch.enable_grad``)
+        before the update and returned, as torch.optim does.
+        """
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        self._pull_groups()
         self.adamw.step()
         self.muon.step()
+        return loss
 
-    def zero_grad(self) -> None:
-        """Zero the gradients of every parameter of both branches."""
-        self.adamw.zero_grad()
-        self.muon.zero_grad()
+    def zero_grad(self, set_to_none: bool = False) -> None:
+        """Zero the gradients of every parameter of both branches (or set them
+        to None with ``set_to_none=True``)."""
+        self.adamw.zero_grad(set_to_none)
+        self.muon.zero_grad(set_to_none)
 
     def state_dict(self) -> dict[str, object]:
-        """The parameter lists of both branches (optimizer.py:166-168)."""
-        return self.param_group
+        """Both branches' optimizer state, ``{"adam": <torch.optim.AdamW format>,
+        "muon": <torch.optim.Muon format>}`` (the format of
+        ``PyTorchMuonAdamW.state_dict()``).  The reference returned only the
+        parameter lists (optimizer.py:166-168); those remain in ``param_group``."""
+        self._pull_groups()
+        return {"adam": self.adamw.state_dict(), "muon": self.muon.state_dict()}
 
     def load_state_dict(self, state_dict: dict[str, object]) -> None:
-        """Reassign the branches' parameter lists (optimizer.py:170-175)."""
+        """Load optimizer state from :meth:`state_dict` or ``PyTorchMuonAdamW.state_dict()``.
+
+        A branch entry that is a list of parameters (the reference's format,
+        optimizer.py:170-175) replaces that branch's parameter list instead.
+        """
         if "adam" in state_dict:
-            self.adamw.model_params = state_dict["adam"]
+            sd = state_dict["adam"]
+            if isinstance(sd, dict):
+                self.adamw.load_state_dict(sd)
+            else:
+                self.adamw.model_params = sd
+                self.param_group["adam"] = sd
         if "muon" in state_dict:
-            self.muon.model_params = state_dict["muon"]
+            sd = state_dict["muon"]
+            if isinstance(sd, dict):
+                self.muon.load_state_dict(sd)
+            else:
+                self.muon.model_params = sd
+                self.param_group["muon"] = sd
+        self._push_groups()
 
 
 class PyTorchMuonAdamW:
@@ -246,15 +317,20 @@ class PyTorchMuonAdamW:
             adjust_lr_fn=muon_config.adjust_lr_fn,
         )
 
-    def step(self) -> None:
-        """Apply one reference AdamW and Muon update."""
+    def step(self, closure=None):
+        """Apply one reference AdamW and Muon update (``closure`` as torch.optim)."""
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
         self.adamw.step()
         self.muon.step()
+        return loss
 
-    def zero_grad(self) -> None:
-        """Reset gradients for both reference optimizers."""
-        self.adamw.zero_grad()
-        self.muon.zero_grad()
+    def zero_grad(self, *args, **kwargs) -> None:
+        """Reset gradients for both reference optimizers (torch's default: to None)."""
+        self.adamw.zero_grad(*args, **kwargs)
+        self.muon.zero_grad(*args, **kwargs)
 
     def state_dict(self) -> dict[str, object]:
         """The serialized state of both torch optimizers."""
