@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MAMW_ABI_VERSION 1
+#define MAMW_ABI_VERSION 2
 
 /* ---- status codes -------------------------------------------------------- */
 #define MAMW_OK             0
@@ -74,6 +74,27 @@ typedef struct mamw_adamw_tensor {
     int64_t      numel;      /* >= 0; 0 is a no-op      */
 } mamw_adamw_tensor;
 
+/* Element-type flags of a tensor (mamw_adamw_tensor_ex.flags) or matrix
+ * (mamw_muon_matrix.flags).  Optimizer state (exp_avg, exp_avg_sq, momentum)
+ * is fp32 in every case; the update is computed in fp32 and a bf16 parameter is
+ * written back rounded to nearest-even.                                         */
+#define MAMW_BF16_PARAM 0x1 /* param holds bf16 (uint16_t bit patterns) */
+#define MAMW_BF16_GRAD  0x2 /* grad holds bf16                           */
+
+/* A tensor of any element-type combination.  No counterpart in the reference
+ * (whose kernels take the parameter's dtype for every buffer,
+ * triton_adam.py:79-85,129-130): bf16 parameters and/or gradients with fp32
+ * moments.                                                                    */
+typedef struct mamw_adamw_tensor_ex {
+    void*        param;      /* numel fp32, or bf16 with MAMW_BF16_PARAM */
+    const void*  grad;       /* numel fp32, or bf16 with MAMW_BF16_GRAD  */
+    float*       exp_avg;    /* numel fp32                                */
+    float*       exp_avg_sq; /* numel fp32                                */
+    int64_t      numel;      /* >= 0; 0 is a no-op                        */
+    int32_t      flags;      /* MAMW_BF16_* bits; other bits rejected     */
+    int32_t      reserved;   /* must be 0                                 */
+} mamw_adamw_tensor_ex;
+
 /* One tensor, one launch.  Replaces solve_adamw_step (triton_adam.py:66-103),
  * which views 1-D tensors as (1,N) and launches a (M, cdiv(N,512)) grid. */
 int mamw_adamw_tensor_step(float* param, const float* grad, float* exp_avg,
@@ -94,6 +115,11 @@ int mamw_adamw_table_bytes(int n_tensors, size_t* bytes);
 int mamw_adamw_table_pack(const mamw_adamw_tensor* tensors, int n_tensors,
                           void* host_table, size_t table_bytes,
                           int64_t* n_blocks);
+/* mamw_adamw_table_pack for mamw_adamw_tensor_ex entries (same table format,
+ * same mamw_adamw_mt_step); bf16 buffers need 2-byte alignment.               */
+int mamw_adamw_table_pack_ex(const mamw_adamw_tensor_ex* tensors, int n_tensors,
+                             void* host_table, size_t table_bytes,
+                             int64_t* n_blocks);
 int mamw_adamw_mt_step(const void* device_table, int n_tensors,
                        int64_t n_blocks, float lr, float bias1, float bias2,
                        float beta1, float beta2, float weight_decay, float eps,
@@ -117,8 +143,9 @@ int mamw_adamw_mt_step(const void* device_table, int n_tensors,
 #define MAMW_MUON_MAX_BATCH 32
 
 typedef struct mamw_muon_matrix {
-    float*       param;     /* rows x cols fp32, row-major, contiguous */
-    const float* grad;      /* rows x cols fp32                        */
+    float*       param;     /* rows x cols fp32, row-major, contiguous
+                               (bf16 with MAMW_BF16_PARAM)             */
+    const float* grad;      /* rows x cols fp32 (bf16 with MAMW_BF16_GRAD) */
     float*       momentum;  /* rows x cols fp32                        */
     float*       update;    /* optional (NULL = skip): receives the orthogonalised
                                update (rows x cols fp32, bf16-valued), the `out`
@@ -126,7 +153,8 @@ typedef struct mamw_muon_matrix {
     int64_t      rows;
     int64_t      cols;
     float        scaled_lr; /* lr * adjust_lr(rows, cols)              */
-    int32_t      reserved;  /* must be 0                               */
+    int32_t      flags;     /* MAMW_BF16_* bits (0: fp32 param and grad);
+                               other bits rejected                      */
 } mamw_muon_matrix;
 
 int mamw_muon_workspace_bytes(int batch, int64_t rows, int64_t cols,

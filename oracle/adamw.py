@@ -15,11 +15,20 @@ and the step-loop semantics of ``TritonAdamW.step`` (:132-153): one global
 step counter incremented on every call, bias corrections computed on the
 host in float64 and passed to the kernel as float32, parameters whose grad is
 ``None`` skipped.
+
+bf16 parameters and gradients (no counterpart in the reference, whose kernel
+computes in the parameter's dtype, triton_adam.py:79-85): the values are
+widened exactly, the update above runs in fp32 with fp32 moments, and a bf16
+parameter is rounded back to nearest-even (``param_bf16=True``).  Pinned
+against torch.optim.AdamW in fp32 with the parameter rounded to bf16 after
+every step.
 """
 
 from __future__ import annotations
 
 import numpy as np
+
+from .bf16 import round_bf16
 
 F32 = np.float32
 
@@ -29,8 +38,12 @@ def bias_corrections(beta1: float, beta2: float, step: int) -> tuple[np.float32,
     return F32(1 - beta1**step), F32(1 - beta2**step)
 
 
-def adamw_update(p, g, m, v, *, lr, bias1, bias2, beta1, beta2, weight_decay, eps):
-    """One AdamW update of float32 arrays; returns new (p, m, v) (triton_adam.py:53-59)."""
+def adamw_update(p, g, m, v, *, lr, bias1, bias2, beta1, beta2, weight_decay, eps, param_bf16=False):
+    """One AdamW update of float32 arrays; returns new (p, m, v) (triton_adam.py:53-59).
+
+    ``param_bf16``: the parameter is bf16 (its bf16 values arrive as float32);
+    the new value is rounded to bf16 (returned as float32).
+    """
     p = np.asarray(p, dtype=F32)
     g = np.asarray(g, dtype=F32)
     m = np.asarray(m, dtype=F32)
@@ -44,6 +57,8 @@ def adamw_update(p, g, m, v, *, lr, bias1, bias2, beta1, beta2, weight_decay, ep
     v_c = v_t / bias2
     p_decay = (one - lr * wd) * p
     p_new = p_decay - lr * (m_c / (np.sqrt(v_c) + eps))
+    if param_bf16:
+        p_new = round_bf16(p_new.astype(F32))
     return p_new.astype(F32), m_t.astype(F32), v_t.astype(F32)
 
 
@@ -54,8 +69,9 @@ class AdamWOracle:
     to :meth:`step` is a parallel list whose entries may be ``None``.
     """
 
-    def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), weight_decay=1e-2, eps=1e-7):
+    def __init__(self, params, lr=1e-3, betas=(0.9, 0.999), weight_decay=1e-2, eps=1e-7, param_bf16=False):
         self.params = params
+        self.param_bf16 = param_bf16
         self.lr, self.beta1, self.beta2 = lr, betas[0], betas[1]
         self.weight_decay, self.eps = weight_decay, eps
         self.step_num = 0
@@ -70,5 +86,6 @@ class AdamWOracle:
                 continue
             p_new, self.m[i], self.v[i] = adamw_update(
                 p, g, self.m[i], self.v[i], lr=self.lr, bias1=bias1, bias2=bias2,
-                beta1=self.beta1, beta2=self.beta2, weight_decay=self.weight_decay, eps=self.eps)
+                beta1=self.beta1, beta2=self.beta2, weight_decay=self.weight_decay, eps=self.eps,
+                param_bf16=self.param_bf16)
             p[...] = p_new

@@ -109,8 +109,14 @@ def zeropower_ns(G, coeffs=(3.4445, -4.7750, 2.0315), ns_steps=5, eps=1e-7, exac
 
 
 def muon_update(param, grad, momentum, *, lr, weight_decay, beta, nesterov=True,
-                coeffs=(3.4445, -4.7750, 2.0315), ns_steps=5, eps=1e-7, adjust_lr_fn="original"):
-    """One Muon update; returns (new_param, new_momentum, orthogonalised update)."""
+                coeffs=(3.4445, -4.7750, 2.0315), ns_steps=5, eps=1e-7, adjust_lr_fn="original",
+                param_bf16=False):
+    """One Muon update; returns (new_param, new_momentum, orthogonalised update).
+
+    ``param_bf16``: the parameter is bf16 (values arrive as float32); the
+    update runs in fp32 with an fp32 momentum and the new parameter is rounded
+    to bf16.  A bf16 gradient needs nothing: its values are exact in fp32.
+    """
     param = np.asarray(param, dtype=F32)
     grad = np.asarray(grad, dtype=F32)
     mom = lerp(momentum, grad, 1 - beta)
@@ -119,6 +125,8 @@ def muon_update(param, grad, momentum, *, lr, weight_decay, beta, nesterov=True,
     adj = adjust_lr(lr, adjust_lr_fn, param.shape)
     p = param * F32(1 - lr * weight_decay)
     p = fma32(F32(-adj), O, p)
+    if param_bf16:
+        p = round_bf16(np.asarray(p, dtype=F32))
     return p, mom, O
 
 
@@ -126,10 +134,11 @@ class MuonOracle:
     """CPU model of one Muon branch (triton_muon.py:375-448) on numpy arrays."""
 
     def __init__(self, params, lr=1e-3, weight_decay=0.1, coeffs=(3.445, -4.775, 2.0315),
-                 nesterov=True, beta=0.95, ns_steps=5, eps=1e-7, adjust_lr_fn="original"):
+                 nesterov=True, beta=0.95, ns_steps=5, eps=1e-7, adjust_lr_fn="original", param_bf16=False):
         self.params = params
         self.kw = dict(lr=lr, weight_decay=weight_decay, beta=beta, nesterov=nesterov,
-                       coeffs=coeffs, ns_steps=ns_steps, eps=eps, adjust_lr_fn=adjust_lr_fn)
+                       coeffs=coeffs, ns_steps=ns_steps, eps=eps, adjust_lr_fn=adjust_lr_fn,
+                       param_bf16=param_bf16)
         self.momentum = [np.zeros_like(p, dtype=F32) for p in params]
 
     def step(self, grads):

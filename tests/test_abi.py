@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_strerror():
     lib = _lib.load()
-    assert lib.mamw_abi_version() == 1
+    assert lib.mamw_abi_version() == 2
     for code in (OK, NULL, COUNT, NUMEL, SHAPE, ALIGN, WS, HYPER, TABLE, ALIAS):
         msg = lib.mamw_strerror(code).decode()
         assert msg and msg != "unknown status"
@@ -77,6 +77,52 @@ def test_adamw_pack_blocks_and_records():
     assert vec_ok == [1, 1, 1, 1]
     st, buf, _ = _pack([_t((1 << 40) + 4, 100)])  # 4-byte aligned, not 16
     assert st == OK and struct.unpack_from("<i", buf, 48)[0] == 0
+
+
+def _pack_ex(entries):
+    lib = _lib.load()
+    n = len(entries)
+    arr = (_lib.AdamWTensorEx * max(n, 1))(*entries)
+    buf = (ctypes.c_uint8 * max(64 * n, 1))()
+    blocks = ctypes.c_int64(-1)
+    st = lib.mamw_adamw_table_pack_ex(arr, n, buf, 64 * n, ctypes.byref(blocks))
+    return st, bytes(buf), blocks.value
+
+
+def _tx(base, numel, flags, pstep=1 << 30):
+    return _lib.AdamWTensorEx(base, base + pstep, base + 2 * pstep, base + 3 * pstep, numel, flags, 0)
+
+
+def test_adamw_pack_ex_flags_and_alignment():
+    import struct
+
+    BP, BG = _lib.BF16_PARAM, _lib.BF16_GRAD
+    st, buf, blocks = _pack_ex([_tx(1 << 40, 2048, BP), _tx(2 << 40, 1, BG), _tx(3 << 40, 5, BP | BG)])
+    assert st == OK and blocks == 2 + 1 + 1
+    assert [struct.unpack_from("<i", buf, 64 * i + 52)[0] for i in range(3)] == [BP, BG, BP | BG]
+    # bf16 buffers need 2-byte alignment, and 8 bytes for the vector path
+    e = _lib.AdamWTensorEx((1 << 40) + 8, 2 << 40, 3 << 40, 4 << 40, 100, BP, 0)
+    st, buf, _ = _pack_ex([e])  # bf16 param 8-aligned, fp32 buffers 16-aligned: vector path
+    assert st == OK and struct.unpack_from("<i", buf, 48)[0] == 1
+    st, buf, _ = _pack_ex([_tx((1 << 40) + 2, 100, BP | BG, pstep=(1 << 30) + 2)])
+    assert st == ALIGN  # exp_avg would be 2-byte aligned (fp32 needs 4)
+    e = _lib.AdamWTensorEx((1 << 40) + 2, 2 << 40, 3 << 40, 4 << 40, 100, BP, 0)
+    st, buf, _ = _pack_ex([e])
+    assert st == OK and struct.unpack_from("<i", buf, 48)[0] == 0  # bf16 param 2-aligned: scalar path
+    e = _lib.AdamWTensorEx((1 << 40) + 1, 2 << 40, 3 << 40, 4 << 40, 100, BP, 0)
+    assert _pack_ex([e])[0] == ALIGN
+
+
+def test_adamw_pack_ex_rejects():
+    BP = _lib.BF16_PARAM
+    assert _pack_ex([_tx(1 << 40, 10, 4)])[0] == HYPER  # unknown flag bit
+    e = _lib.AdamWTensorEx(1 << 40, 2 << 40, 3 << 40, 4 << 40, 10, 0, 1)
+    assert _pack_ex([e])[0] == HYPER  # reserved != 0
+    # overlap computed with the bf16 size: a bf16 param of 100 elements ends 200 bytes on
+    e = _lib.AdamWTensorEx(1 << 40, (1 << 40) + 200, 3 << 40, 4 << 40, 100, BP, 0)
+    assert _pack_ex([e])[0] == OK
+    e = _lib.AdamWTensorEx(1 << 40, (1 << 40) + 196, 3 << 40, 4 << 40, 100, BP, 0)
+    assert _pack_ex([e])[0] == ALIAS
 
 
 @pytest.mark.parametrize("bad,code", [
@@ -170,7 +216,7 @@ def test_muon_step_rejects_before_hip():
     assert _step(arr, 2, ws_bytes=1000) == WS
     assert _step(arr, 0) == COUNT
     assert _step(arr, 2, steps=100) == HYPER
-    arr[1].reserved = 1
+    arr[1].flags = 4  # not a MAMW_BF16_* bit
     assert _step(arr, 2) == HYPER
     arr = _mats([(256, 512), (512, 256)])
     arr[1].param = arr[0].param  # two entries update the same parameter

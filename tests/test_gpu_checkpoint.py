@@ -143,3 +143,36 @@ def test_step_closure_returns_loss(gpu):
     torch.cuda.synchronize()
     assert torch.is_tensor(loss) and loss.item() > 0
     assert not torch.equal(before, w.detach())  # only w has a gradient; it moved
+
+
+def test_grad_scaler_unscales_and_skips_inf_steps(gpu):
+    """torch.amp.GradScaler drives MuonAdamW like any torch optimizer: gradients
+    are unscaled in place (power-of-two scale: exact) before step(); a step with
+    a non-finite gradient is skipped entirely (parameters, state and the AdamW
+    step counter untouched), as torch.optim does."""
+    a, b = _params(gpu), _params(gpu)
+    opt_a = MuonAdamW(_split(a), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    opt_b = MuonAdamW(_split(b), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    scaler = torch.amp.GradScaler("cuda", init_scale=1024.0, growth_interval=1000)
+    scaler.scale(torch.ones((), device=gpu))  # initialise the scale on the device
+    gen = torch.Generator(device=gpu).manual_seed(4)
+    g = _grads(a, gpu, gen)
+    for (_, p, _), gi in zip(a, g):
+        p.grad = gi * 1024.0
+    _set(b, g)
+    scaler.step(opt_a)
+    scaler.update()
+    opt_b.step()
+    torch.cuda.synchronize()
+    for (n, p, _), (_, q, _) in zip(a, b):
+        assert torch.equal(p.detach(), q.detach()), n
+    before = [p.detach().clone() for _, p, _ in a]
+    g = _grads(a, gpu, gen)
+    g[0][0] = float("inf")
+    for (_, p, _), gi in zip(a, g):
+        p.grad = gi * scaler.get_scale()
+    scaler.step(opt_a)
+    scaler.update()
+    torch.cuda.synchronize()
+    assert all(torch.equal(p.detach(), q) for (_, p, _), q in zip(a, before))
+    assert opt_a.adamw.step_num == 1 and scaler.get_scale() == 512.0

@@ -130,3 +130,43 @@ def test_planted_mistakes_are_caught(kind):
     mp, _, _ = _oracle_run(p0, grads, 5, update=_mutant(kind))
     with pytest.raises(AssertionError):
         np.testing.assert_allclose(mp, tp, rtol=0, atol=1e-7)
+
+
+# --- bf16 parameters / gradients (fp32 moments) --------------------------------
+
+def _bf16(x):
+    return torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).bfloat16().float().numpy()
+
+
+def test_bf16_param_matches_torch_fp32_rounded_each_step():
+    """The bf16 semantics (fp32 update and moments, parameter rounded to bf16 after
+    every step) equal torch's fp32 AdamW with the parameter rounded each step."""
+    p0 = _bf16(_rand(100000, 0.02, 21))
+    grads = [_bf16(_rand(100000, 1e-3, 30 + i)) for i in range(6)]
+    tp = torch.nn.Parameter(torch.from_numpy(p0.copy()))
+    opt = torch.optim.AdamW([tp], lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, eps=1e-8, fused=True)
+    o = oa.AdamWOracle([p0.copy()], lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, eps=1e-8, param_bf16=True)
+    for g in grads:
+        tp.grad = torch.from_numpy(g.copy())
+        opt.step()
+        with torch.no_grad():
+            tp.copy_(tp.bfloat16().float())
+        o.step([g])
+    t = tp.detach().numpy()
+    got = o.params[0]
+    assert np.array_equal(_bf16(got), got)  # every value is a bf16
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(t), 1e-30))) - 7)
+    assert (np.abs(got - t) <= ulp).all()
+    assert (got == t).mean() > 0.999  # torch's fp32 rounding differs by ~1e-7: rare boundary flips only
+    np.testing.assert_allclose(o.m[0], opt.state[tp]["exp_avg"].numpy(), rtol=0, atol=1e-9)
+
+
+def test_bf16_planted_missing_rounding_is_caught():
+    p0 = _bf16(_rand(20000, 0.02, 22))
+    g = _bf16(_rand(20000, 1e-3, 23))
+    b1, b2 = oa.bias_corrections(0.9, 0.95, 1)
+    z = np.zeros_like(p0)
+    good, _, _ = oa.adamw_update(p0, g, z, z, bias1=b1, bias2=b2, param_bf16=True, **HP)
+    bad, _, _ = oa.adamw_update(p0, g, z, z, bias1=b1, bias2=b2, param_bf16=False, **HP)
+    assert np.array_equal(_bf16(good), good)
+    assert not np.array_equal(_bf16(bad), bad)  # an unrounded parameter is not a bf16 tensor

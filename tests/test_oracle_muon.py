@@ -187,3 +187,27 @@ def test_planted_momentum_mistake_is_caught():
     t = torch.from_numpy(s).lerp(torch.from_numpy(e), 0.05).numpy()
     wrong = om.lerp(e, s, 0.05)  # start and end swapped
     assert not np.allclose(wrong, t, rtol=1e-3, atol=0)
+
+
+def test_bf16_param_step_matches_torch_fp32_rounded():
+    """bf16 parameter and gradient with an fp32 momentum: torch.optim.Muon in fp32
+    on the bf16 values, the parameter rounded to bf16 after the step."""
+    rng = np.random.default_rng(9)
+    shape = (64, 96)
+    p0 = bf16.round_bf16((rng.standard_normal(shape) * 0.02).astype(np.float32))
+    g = bf16.round_bf16(rng.standard_normal(shape).astype(np.float32))
+    m0 = (rng.standard_normal(shape) * 1e-3).astype(np.float32)
+    tp = torch.nn.Parameter(torch.from_numpy(p0.copy()))
+    opt = torch.optim.Muon([tp], lr=0.02, weight_decay=0.1, momentum=0.95, nesterov=True,
+                           ns_coefficients=COEFFS, eps=1e-7, ns_steps=5, adjust_lr_fn="original")
+    opt.state[tp]["momentum_buffer"] = torch.from_numpy(m0.copy())
+    tp.grad = torch.from_numpy(g.copy())
+    opt.step()
+    t = tp.detach().bfloat16().float().numpy()
+    op, om_, _ = om.muon_update(p0, g, m0, lr=0.02, weight_decay=0.1, beta=0.95, nesterov=True,
+                                coeffs=COEFFS, ns_steps=5, eps=1e-7, param_bf16=True)
+    assert np.array_equal(om_, opt.state[tp]["momentum_buffer"].numpy())
+    assert np.array_equal(bf16.round_bf16(op), op)
+    adj = om.adjust_lr(0.02, "original", shape)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(t), 1e-30))) - 7)
+    assert (np.abs(op - t) <= ulp + adj * 8e-3).all()

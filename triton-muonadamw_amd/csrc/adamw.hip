@@ -69,25 +69,64 @@ __device__ __forceinline__ void adamw_vec(float4& p, float4 g, float4& m, float4
     adamw_elem(p.w, g.w, m.w, v.w, c);
 }
 
-// Update elements [start, start + len) of tensor r (len <= kAdamWChunk).
+// 4-element groups of a parameter or gradient buffer: fp32 (16 bytes) or bf16
+// (8 bytes, widened exactly; stores round to nearest-even).
+template <bool BF16>
+__device__ __forceinline__ float4 ld4(const void* base, int64_t i) {
+    if constexpr (BF16) {
+        typedef unsigned int nt_u2 __attribute__((ext_vector_type(2)));
+        const nt_u2 w = __builtin_nontemporal_load(reinterpret_cast<const nt_u2*>(base) + i);
+        return make_float4(bf16_to_f32(w.x & 0xffffu), bf16_to_f32(w.x >> 16), bf16_to_f32(w.y & 0xffffu),
+                           bf16_to_f32(w.y >> 16));
+    } else {
+        return nt_load(reinterpret_cast<const float4*>(base) + i);
+    }
+}
+template <bool BF16>
+__device__ __forceinline__ void st4(void* base, int64_t i, float4 x) {
+    if constexpr (BF16) {
+        typedef unsigned int nt_u2 __attribute__((ext_vector_type(2)));
+        const nt_u2 w = {pack_bf16x2(x.x, x.y), pack_bf16x2(x.z, x.w)};
+        __builtin_nontemporal_store(w, reinterpret_cast<nt_u2*>(base) + i);
+    } else {
+        nt_store(reinterpret_cast<float4*>(base) + i, x);
+    }
+}
+template <bool BF16>
+__device__ __forceinline__ float ld1(const void* base, int64_t i) {
+    if constexpr (BF16)
+        return bf16_to_f32(reinterpret_cast<const uint16_t*>(base)[i]);
+    else
+        return reinterpret_cast<const float*>(base)[i];
+}
+template <bool BF16>
+__device__ __forceinline__ void st1(void* base, int64_t i, float x) {
+    if constexpr (BF16)
+        reinterpret_cast<uint16_t*>(base)[i] = uint16_t(f32_to_bf16(x));
+    else
+        reinterpret_cast<float*>(base)[i] = x;
+}
+
+// Update elements [start, start + len) of tensor r (len <= kAdamWChunk); PB /
+// GB: the parameter / gradient hold bf16.  The arithmetic is the fp32 one in
+// every case.
+template <bool PB, bool GB>
 __device__ __forceinline__ void adamw_chunk(const AdamWRec& r, int64_t start, int len,
                                             const AdamWConsts& c) {
     const int tid = threadIdx.x;
-    float* __restrict__ P = r.p + start;
-    const float* __restrict__ G = r.g + start;
     float* __restrict__ M = r.m + start;
     float* __restrict__ V = r.v + start;
+    float4* M4 = reinterpret_cast<float4*>(M);
+    float4* V4 = reinterpret_cast<float4*>(V);
+    // Vector index i covers elements start + 4i .. +3 (start is a multiple of 4).
+    const int64_t q0 = start >> 2;
     if (r.vec_ok && len == kAdamWChunk) {
-        float4* P4 = reinterpret_cast<float4*>(P);
-        const float4* G4 = reinterpret_cast<const float4*>(G);
-        float4* M4 = reinterpret_cast<float4*>(M);
-        float4* V4 = reinterpret_cast<float4*>(V);
         float4 p[kAdamWUnroll], g[kAdamWUnroll], m[kAdamWUnroll], v[kAdamWUnroll];
 #pragma unroll
         for (int u = 0; u < kAdamWUnroll; ++u) {
             const int i = u * kAdamWThreads + tid;
-            p[u] = nt_load(P4 + i);
-            g[u] = nt_load(G4 + i);
+            p[u] = ld4<PB>(r.p, q0 + i);
+            g[u] = ld4<GB>(r.g, q0 + i);
             m[u] = nt_load(M4 + i);
             v[u] = nt_load(V4 + i);
         }
@@ -95,7 +134,7 @@ __device__ __forceinline__ void adamw_chunk(const AdamWRec& r, int64_t start, in
         for (int u = 0; u < kAdamWUnroll; ++u) {
             const int i = u * kAdamWThreads + tid;
             adamw_vec(p[u], g[u], m[u], v[u], c);
-            nt_store(P4 + i, p[u]);
+            st4<PB>(r.p, q0 + i, p[u]);
             nt_store(M4 + i, m[u]);
             nt_store(V4 + i, v[u]);
         }
@@ -104,25 +143,32 @@ __device__ __forceinline__ void adamw_chunk(const AdamWRec& r, int64_t start, in
     int scalar_from = 0;
     if (r.vec_ok) {
         const int nv = len >> 2;
-        float4* P4 = reinterpret_cast<float4*>(P);
-        const float4* G4 = reinterpret_cast<const float4*>(G);
-        float4* M4 = reinterpret_cast<float4*>(M);
-        float4* V4 = reinterpret_cast<float4*>(V);
         for (int i = tid; i < nv; i += kAdamWThreads) {
-            float4 p = nt_load(P4 + i), m = nt_load(M4 + i), v = nt_load(V4 + i);
-            adamw_vec(p, nt_load(G4 + i), m, v, c);
-            nt_store(P4 + i, p);
+            float4 p = ld4<PB>(r.p, q0 + i), m = nt_load(M4 + i), v = nt_load(V4 + i);
+            adamw_vec(p, ld4<GB>(r.g, q0 + i), m, v, c);
+            st4<PB>(r.p, q0 + i, p);
             nt_store(M4 + i, m);
             nt_store(V4 + i, v);
         }
         scalar_from = nv << 2;
     }
     for (int e = scalar_from + tid; e < len; e += kAdamWThreads) {
-        float p = P[e], m = M[e], v = V[e];
-        adamw_elem(p, G[e], m, v, c);
-        P[e] = p;
+        float p = ld1<PB>(r.p, start + e), m = M[e], v = V[e];
+        adamw_elem(p, ld1<GB>(r.g, start + e), m, v, c);
+        st1<PB>(r.p, start + e, p);
         M[e] = m;
         V[e] = v;
+    }
+}
+
+// The block's chunk, dispatched on the tensor's element types (uniform per block).
+__device__ __forceinline__ void adamw_chunk_any(const AdamWRec& r, int64_t start, int len,
+                                                const AdamWConsts& c) {
+    switch (r.flags & (MAMW_BF16_PARAM | MAMW_BF16_GRAD)) {
+        case 0: adamw_chunk<false, false>(r, start, len, c); break;
+        case MAMW_BF16_PARAM: adamw_chunk<true, false>(r, start, len, c); break;
+        case MAMW_BF16_GRAD: adamw_chunk<false, true>(r, start, len, c); break;
+        default: adamw_chunk<true, true>(r, start, len, c); break;
     }
 }
 
@@ -141,13 +187,13 @@ __global__ __launch_bounds__(kAdamWThreads) void adamw_mt_kernel(const AdamWRec*
     const AdamWRec r = recs[lo];
     const int64_t start = (b - r.block_begin) * kAdamWChunk;
     const int64_t rem = r.numel - start;
-    adamw_chunk(r, start, rem < kAdamWChunk ? int(rem) : int(kAdamWChunk), c);
+    adamw_chunk_any(r, start, rem < kAdamWChunk ? int(rem) : int(kAdamWChunk), c);
 }
 
 __global__ __launch_bounds__(kAdamWThreads) void adamw_one_kernel(AdamWRec r, AdamWConsts c) {
     const int64_t start = int64_t(blockIdx.x) * kAdamWChunk;
     const int64_t rem = r.numel - start;
-    adamw_chunk(r, start, rem < kAdamWChunk ? int(rem) : int(kAdamWChunk), c);
+    adamw_chunk_any(r, start, rem < kAdamWChunk ? int(rem) : int(kAdamWChunk), c);
 }
 
 }  // namespace
@@ -177,6 +223,11 @@ extern "C" int mamw_adamw_table_bytes(int n_tensors, size_t* bytes) {
 extern "C" int mamw_adamw_table_pack(const mamw_adamw_tensor* tensors, int n_tensors,
                                      void* host_table, size_t table_bytes, int64_t* n_blocks) {
     return adamw_table_pack(tensors, n_tensors, host_table, table_bytes, n_blocks);
+}
+
+extern "C" int mamw_adamw_table_pack_ex(const mamw_adamw_tensor_ex* tensors, int n_tensors,
+                                        void* host_table, size_t table_bytes, int64_t* n_blocks) {
+    return adamw_table_pack_ex(tensors, n_tensors, host_table, table_bytes, n_blocks);
 }
 
 extern "C" int mamw_adamw_mt_step(const void* device_table, int n_tensors, int64_t n_blocks,

@@ -20,21 +20,23 @@ bool overlap(const void* a, size_t na, const void* b, size_t nb) {
 // ---------------------------------------------------------------------------
 // AdamW
 
-int adamw_validate_tensor(const mamw_adamw_tensor& t) {
+int adamw_validate_tensor(const mamw_adamw_tensor_ex& t) {
+    if (t.flags & ~(MAMW_BF16_PARAM | MAMW_BF16_GRAD) || t.reserved != 0) return MAMW_ERR_HYPER;
     if (t.numel < 0 || t.numel > kMaxNumel) return MAMW_ERR_NUMEL;
     if (t.numel == 0) return MAMW_OK;
     if (!t.param || !t.grad || !t.exp_avg || !t.exp_avg_sq) return MAMW_ERR_NULL;
-    if (!aligned(t.param, 4) || !aligned(t.grad, 4) || !aligned(t.exp_avg, 4) ||
-        !aligned(t.exp_avg_sq, 4))
+    const size_t ep = (t.flags & MAMW_BF16_PARAM) ? 2 : 4, eg = (t.flags & MAMW_BF16_GRAD) ? 2 : 4;
+    if (!aligned(t.param, ep) || !aligned(t.grad, eg) || !aligned(t.exp_avg, 4) || !aligned(t.exp_avg_sq, 4))
         return MAMW_ERR_ALIGN;
     // param, exp_avg, exp_avg_sq are written: they must not overlap each other
     // or the gradient.
-    const size_t nb = size_t(t.numel) * sizeof(float);
+    const size_t n = size_t(t.numel);
     const void* w[3] = {t.param, t.exp_avg, t.exp_avg_sq};
+    const size_t wb[3] = {n * ep, n * 4, n * 4};
     for (int i = 0; i < 3; ++i) {
-        if (overlap(w[i], nb, t.grad, nb)) return MAMW_ERR_ALIAS;
+        if (overlap(w[i], wb[i], t.grad, n * eg)) return MAMW_ERR_ALIAS;
         for (int j = i + 1; j < 3; ++j)
-            if (overlap(w[i], nb, w[j], nb)) return MAMW_ERR_ALIAS;
+            if (overlap(w[i], wb[i], w[j], wb[j])) return MAMW_ERR_ALIAS;
     }
     return MAMW_OK;
 }
@@ -46,8 +48,8 @@ int adamw_table_bytes(int n_tensors, size_t* bytes) {
     return MAMW_OK;
 }
 
-int adamw_table_pack(const mamw_adamw_tensor* tensors, int n_tensors, void* host_table,
-                     size_t table_bytes, int64_t* n_blocks) {
+int adamw_table_pack_ex(const mamw_adamw_tensor_ex* tensors, int n_tensors, void* host_table,
+                        size_t table_bytes, int64_t* n_blocks) {
     if (!n_blocks) return MAMW_ERR_NULL;
     if (n_tensors < 0 || n_tensors > kMaxTensors) return MAMW_ERR_COUNT;
     if (n_tensors > 0 && (!tensors || !host_table)) return MAMW_ERR_NULL;
@@ -55,7 +57,7 @@ int adamw_table_pack(const mamw_adamw_tensor* tensors, int n_tensors, void* host
     AdamWRec* rec = static_cast<AdamWRec*>(host_table);
     int64_t blocks = 0;
     for (int i = 0; i < n_tensors; ++i) {
-        const mamw_adamw_tensor& t = tensors[i];
+        const mamw_adamw_tensor_ex& t = tensors[i];
         int st = adamw_validate_tensor(t);
         if (st != MAMW_OK) return st;
         AdamWRec r;
@@ -66,11 +68,37 @@ int adamw_table_pack(const mamw_adamw_tensor* tensors, int n_tensors, void* host
         r.v = t.exp_avg_sq;
         r.numel = t.numel;
         r.block_begin = blocks;
-        r.vec_ok = aligned(t.param, 16) && aligned(t.grad, 16) && aligned(t.exp_avg, 16) &&
+        r.flags = t.flags;
+        // 4 elements per vector access: 16 bytes of fp32, 8 of bf16.
+        r.vec_ok = aligned(t.param, (t.flags & MAMW_BF16_PARAM) ? 8 : 16) &&
+                   aligned(t.grad, (t.flags & MAMW_BF16_GRAD) ? 8 : 16) && aligned(t.exp_avg, 16) &&
                    aligned(t.exp_avg_sq, 16);
         memcpy(&rec[i], &r, sizeof(r));
         blocks += (t.numel + kAdamWChunk - 1) / kAdamWChunk;
         if (blocks > int64_t(0x7fffffff)) return MAMW_ERR_NUMEL;  // grid.x limit
+    }
+    *n_blocks = blocks;
+    return MAMW_OK;
+}
+
+int adamw_table_pack(const mamw_adamw_tensor* tensors, int n_tensors, void* host_table, size_t table_bytes,
+                     int64_t* n_blocks) {
+    if (!n_blocks) return MAMW_ERR_NULL;
+    if (n_tensors < 0 || n_tensors > kMaxTensors) return MAMW_ERR_COUNT;
+    if (n_tensors > 0 && (!tensors || !host_table)) return MAMW_ERR_NULL;
+    if (table_bytes < size_t(n_tensors) * sizeof(AdamWRec)) return MAMW_ERR_TABLE;
+    // fp32 entries are packed one at a time through the general path (no allocation).
+    AdamWRec* rec = static_cast<AdamWRec*>(host_table);
+    int64_t blocks = 0;
+    for (int i = 0; i < n_tensors; ++i) {
+        const mamw_adamw_tensor& t = tensors[i];
+        const mamw_adamw_tensor_ex e{t.param, t.grad, t.exp_avg, t.exp_avg_sq, t.numel, 0, 0};
+        int64_t nb = 0;
+        int st = adamw_table_pack_ex(&e, 1, &rec[i], sizeof(AdamWRec), &nb);
+        if (st != MAMW_OK) return st;
+        rec[i].block_begin = blocks;
+        blocks += nb;
+        if (blocks > int64_t(0x7fffffff)) return MAMW_ERR_NUMEL;
     }
     *n_blocks = blocks;
     return MAMW_OK;
@@ -135,31 +163,32 @@ int muon_validate(const mamw_muon_matrix* mats, int batch, int ns_steps, const v
     memset(descs, 0, sizeof(*descs));
     for (int i = 0; i < batch; ++i) {
         const mamw_muon_matrix& M = mats[i];
-        if (M.reserved != 0) return MAMW_ERR_HYPER;
+        if (M.flags & ~(MAMW_BF16_PARAM | MAMW_BF16_GRAD)) return MAMW_ERR_HYPER;
         if (M.rows < 1 || M.cols < 1) return MAMW_ERR_SHAPE;
         const int64_t mi = M.rows < M.cols ? M.rows : M.cols;
         const int64_t ni = M.rows < M.cols ? M.cols : M.rows;
         if (mi != plan->m || ni != plan->n) return MAMW_ERR_SHAPE;
         if (!M.param || !M.grad || !M.momentum) return MAMW_ERR_NULL;
-        if (!aligned(M.param, 4) || !aligned(M.grad, 4) || !aligned(M.momentum, 4))
-            return MAMW_ERR_ALIGN;
-        const size_t nb = size_t(M.rows) * size_t(M.cols) * 4;
-        if (overlap(M.param, nb, M.grad, nb) || overlap(M.param, nb, M.momentum, nb) ||
-            overlap(M.momentum, nb, M.grad, nb))
+        const size_t ep = (M.flags & MAMW_BF16_PARAM) ? 2 : 4, eg = (M.flags & MAMW_BF16_GRAD) ? 2 : 4;
+        if (!aligned(M.param, ep) || !aligned(M.grad, eg) || !aligned(M.momentum, 4)) return MAMW_ERR_ALIGN;
+        const size_t ne = size_t(M.rows) * size_t(M.cols);
+        const size_t nb = ne * 4, np_ = ne * ep, ng = ne * eg;
+        if (overlap(M.param, np_, M.grad, ng) || overlap(M.param, np_, M.momentum, nb) ||
+            overlap(M.momentum, nb, M.grad, ng))
             return MAMW_ERR_ALIAS;
-        if (overlap(M.param, nb, workspace, plan->bytes) ||
-            overlap(M.momentum, nb, workspace, plan->bytes) ||
-            overlap(M.grad, nb, workspace, plan->bytes))
+        if (overlap(M.param, np_, workspace, plan->bytes) || overlap(M.momentum, nb, workspace, plan->bytes) ||
+            overlap(M.grad, ng, workspace, plan->bytes))
             return MAMW_ERR_ALIAS;
         if (M.update) {
             if (!aligned(M.update, 4)) return MAMW_ERR_ALIGN;
-            if (overlap(M.update, nb, M.param, nb) || overlap(M.update, nb, M.grad, nb) ||
+            if (overlap(M.update, nb, M.param, np_) || overlap(M.update, nb, M.grad, ng) ||
                 overlap(M.update, nb, M.momentum, nb) || overlap(M.update, nb, workspace, plan->bytes))
                 return MAMW_ERR_ALIAS;
         }
         for (int j = 0; j < i; ++j) {  // two entries updating the same memory race
-            const size_t nj = size_t(mats[j].rows) * size_t(mats[j].cols) * 4;
-            if (overlap(M.param, nb, mats[j].param, nj) || overlap(M.momentum, nb, mats[j].momentum, nj))
+            const size_t nej = size_t(mats[j].rows) * size_t(mats[j].cols);
+            const size_t npj = nej * ((mats[j].flags & MAMW_BF16_PARAM) ? 2 : 4);
+            if (overlap(M.param, np_, mats[j].param, npj) || overlap(M.momentum, nb, mats[j].momentum, nej * 4))
                 return MAMW_ERR_ALIAS;
         }
         MuonMatDesc& d = descs->d[i];
@@ -171,6 +200,7 @@ int muon_validate(const mamw_muon_matrix* mats, int batch, int ns_steps, const v
         d.cols = M.cols;
         d.slr = M.scaled_lr;
         d.tall = M.rows > M.cols ? 1 : 0;
+        d.flags = M.flags;
     }
     return MAMW_OK;
 }

@@ -25,14 +25,15 @@ constexpr int kAdamWUnroll = 1;  // float4 groups per thread per block
 constexpr int64_t kAdamWChunk = int64_t(kAdamWThreads) * 4 * kAdamWUnroll;  // 1024
 
 struct alignas(16) AdamWRec {
-    float* p;
-    const float* g;
+    void* p;         // fp32, or bf16 with MAMW_BF16_PARAM
+    const void* g;   // fp32, or bf16 with MAMW_BF16_GRAD
     float* m;
     float* v;
     int64_t numel;
     int64_t block_begin;
-    int32_t vec_ok;  // all four base pointers 16-byte aligned
-    int32_t pad[3];
+    int32_t vec_ok;  // every base pointer aligned for 4-element vector access
+    int32_t flags;   // MAMW_BF16_* bits
+    int32_t pad[2];
 };
 static_assert(sizeof(AdamWRec) == 64, "AdamWRec must stay 64 bytes");
 
@@ -40,10 +41,12 @@ struct AdamWScalars {
     float lr, bias1, bias2, beta1, beta2, weight_decay, eps;
 };
 
-int adamw_validate_tensor(const mamw_adamw_tensor& t);
+int adamw_validate_tensor(const mamw_adamw_tensor_ex& t);
 int adamw_table_bytes(int n_tensors, size_t* bytes);
 int adamw_table_pack(const mamw_adamw_tensor* tensors, int n_tensors,
                      void* host_table, size_t table_bytes, int64_t* n_blocks);
+int adamw_table_pack_ex(const mamw_adamw_tensor_ex* tensors, int n_tensors,
+                        void* host_table, size_t table_bytes, int64_t* n_blocks);
 
 // ---------------------------------------------------------------------------
 // Muon batch plan.
@@ -68,7 +71,8 @@ struct MuonMatDesc {
     int64_t rows;
     int64_t cols;
     float slr;
-    int32_t tall;  // rows > cols: X = bf16(u)^T
+    int32_t tall;   // rows > cols: X = bf16(u)^T
+    int32_t flags;  // MAMW_BF16_* bits
 };
 
 struct MuonBatchDescs {

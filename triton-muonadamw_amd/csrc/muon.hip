@@ -58,8 +58,10 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
 
     const int cg = tid & 15, rr = tid >> 4;
     const int64_t c = c0 + cg * 4;
-    const bool vec = ((C & 3) == 0) &&
-                     ((reinterpret_cast<uintptr_t>(d.grad) | reinterpret_cast<uintptr_t>(d.mom)) & 15) == 0;
+    const bool gb = (d.flags & MAMW_BF16_GRAD) != 0;  // gradient holds bf16
+    const uint16_t* gh = reinterpret_cast<const uint16_t*>(d.grad);
+    const bool vec = ((C & 3) == 0) && (reinterpret_cast<uintptr_t>(d.grad) & (gb ? 7 : 15)) == 0 &&
+                     (reinterpret_cast<uintptr_t>(d.mom) & 15) == 0;
     float ss = 0.f;
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
@@ -69,9 +71,21 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
         if (r < R && c < C) {
             const int64_t off = r * C + c;
             if (vec) {
-                const float4 g4 = *reinterpret_cast<const float4*>(d.grad + off);
+                float g[4];
+                if (gb) {
+                    const uint2 w = *reinterpret_cast<const uint2*>(gh + off);
+                    g[0] = bf16_to_f32(w.x & 0xffffu);
+                    g[1] = bf16_to_f32(w.x >> 16);
+                    g[2] = bf16_to_f32(w.y & 0xffffu);
+                    g[3] = bf16_to_f32(w.y >> 16);
+                } else {
+                    const float4 g4 = *reinterpret_cast<const float4*>(d.grad + off);
+                    g[0] = g4.x;
+                    g[1] = g4.y;
+                    g[2] = g4.z;
+                    g[3] = g4.w;
+                }
                 float4 m4 = *reinterpret_cast<const float4*>(d.mom + off);
-                const float g[4] = {g4.x, g4.y, g4.z, g4.w};
                 float m[4] = {m4.x, m4.y, m4.z, m4.w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -83,7 +97,7 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     if (c + e < C) {
-                        const float g = d.grad[off + e];
+                        const float g = gb ? bf16_to_f32(gh[off + e]) : d.grad[off + e];
                         const float m = lerp_torch(d.mom[off + e], g, a.w_mom);
                         d.mom[off + e] = m;
                         u[e] = NESTEROV ? lerp_torch(g, m, a.w_nest) : m;
@@ -184,7 +198,12 @@ __global__ __launch_bounds__(256) void muon_apply0_kernel(const MuonBatchDescs d
     for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
         const int64_t r = e / d.cols, c = e % d.cols;
         const float u = bf16_to_f32(d.tall ? X[c * a.np + r] : X[r * a.np + c]);
-        d.param[e] = __builtin_fmaf(-d.slr, u, d.param[e] * keep);
+        if (d.flags & MAMW_BF16_PARAM) {
+            uint16_t* ph = reinterpret_cast<uint16_t*>(d.param);
+            ph[e] = uint16_t(f32_to_bf16(__builtin_fmaf(-d.slr, u, bf16_to_f32(ph[e]) * keep)));
+        } else {
+            d.param[e] = __builtin_fmaf(-d.slr, u, d.param[e] * keep);
+        }
         if (d.upd) d.upd[e] = u;
     }
 }
@@ -309,8 +328,31 @@ __device__ __forceinline__ void apply_chunk(const MuonMatDesc& d, uint4 w, int64
         u[2 * j + 1] = bf16_to_f32(ww[j] >> 16);
     }
     const int64_t idx = prow * d.cols + pcol;
-    float* p = d.param + idx;
     float* up = d.upd ? d.upd + idx : nullptr;
+    if (d.flags & MAMW_BF16_PARAM) {  // bf16 parameter: fp32 arithmetic, rounded back to nearest-even
+        uint16_t* ph = reinterpret_cast<uint16_t*>(d.param) + idx;
+        if (nv == 8 && ((reinterpret_cast<uintptr_t>(ph) | reinterpret_cast<uintptr_t>(up)) & 15) == 0) {
+            const uint4 pw = *reinterpret_cast<const uint4*>(ph);
+            const uint32_t pv[4] = {pw.x, pw.y, pw.z, pw.w};
+            uint32_t o[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                o[j] = pack_bf16x2(__builtin_fmaf(-d.slr, u[2 * j], bf16_to_f32(pv[j] & 0xffffu) * keep),
+                                   __builtin_fmaf(-d.slr, u[2 * j + 1], bf16_to_f32(pv[j] >> 16) * keep));
+            *reinterpret_cast<uint4*>(ph) = make_uint4(o[0], o[1], o[2], o[3]);
+            if (up) {
+                reinterpret_cast<float4*>(up)[0] = make_float4(u[0], u[1], u[2], u[3]);
+                reinterpret_cast<float4*>(up)[1] = make_float4(u[4], u[5], u[6], u[7]);
+            }
+        } else {
+            for (int e = 0; e < nv; ++e) {
+                ph[e] = uint16_t(f32_to_bf16(__builtin_fmaf(-d.slr, u[e], bf16_to_f32(ph[e]) * keep)));
+                if (up) up[e] = u[e];
+            }
+        }
+        return;
+    }
+    float* p = d.param + idx;
     if (nv == 8 && ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(up)) & 15) == 0) {
         float4 p0 = reinterpret_cast<const float4*>(p)[0], p1 = reinterpret_cast<const float4*>(p)[1];
         p0.x = __builtin_fmaf(-d.slr, u[0], p0.x * keep);

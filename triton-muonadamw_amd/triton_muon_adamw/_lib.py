@@ -17,8 +17,10 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libmuonadamw_amd.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 MUON_MAX_BATCH = 32
+BF16_PARAM = 0x1  # MAMW_BF16_PARAM
+BF16_GRAD = 0x2   # MAMW_BF16_GRAD
 
 
 class AdamWTensor(ctypes.Structure):
@@ -33,6 +35,20 @@ class AdamWTensor(ctypes.Structure):
     ]
 
 
+class AdamWTensorEx(ctypes.Structure):
+    """``mamw_adamw_tensor_ex``."""
+
+    _fields_ = [
+        ("param", c_void_p),
+        ("grad", c_void_p),
+        ("exp_avg", c_void_p),
+        ("exp_avg_sq", c_void_p),
+        ("numel", c_int64),
+        ("flags", c_int32),
+        ("reserved", c_int32),
+    ]
+
+
 class MuonMatrix(ctypes.Structure):
     """``mamw_muon_matrix``."""
 
@@ -44,7 +60,7 @@ class MuonMatrix(ctypes.Structure):
         ("rows", c_int64),
         ("cols", c_int64),
         ("scaled_lr", c_float),
-        ("reserved", c_int32),
+        ("flags", c_int32),
     ]
 
 
@@ -71,6 +87,7 @@ _PROTOTYPES = {
     ),
     "mamw_adamw_table_bytes": (c_int, [c_int, POINTER(c_size_t)]),
     "mamw_adamw_table_pack": (c_int, [POINTER(AdamWTensor), c_int, c_void_p, c_size_t, POINTER(c_int64)]),
+    "mamw_adamw_table_pack_ex": (c_int, [POINTER(AdamWTensorEx), c_int, c_void_p, c_size_t, POINTER(c_int64)]),
     "mamw_adamw_mt_step": (
         c_int,
         [c_void_p, c_int, c_int64, c_float, c_float, c_float, c_float, c_float, c_float, c_float,
@@ -130,6 +147,15 @@ def check(status: int, what: str) -> None:
     if status < 0:
         raise ValueError(msg)
     raise RuntimeError(msg)
+
+
+def dtype_flag(t: torch.Tensor, bit: int, name: str) -> int:
+    """``bit`` when ``t`` holds bf16, 0 for fp32; other dtypes are an error."""
+    if t.dtype == torch.bfloat16:
+        return bit
+    if t.dtype == torch.float32:
+        return 0
+    raise TypeError(f"{name} must be float32 or bfloat16 (got {t.dtype})")
 
 
 def require_gpu_tensor(t: torch.Tensor, name: str) -> None:

@@ -16,7 +16,11 @@ Where the reference launches one kernel per parameter, ``step()`` launches
 one kernel for all of them (``mamw_adamw_mt_step``).  The packed tensor table
 lives in device memory and is rebuilt only when a parameter or gradient
 pointer changes.  Parameters may have any number of dimensions (the reference
-handles 1-D and 2-D only); they must be contiguous float32 on a ROCm device.
+handles 1-D and 2-D only); they must be contiguous on a ROCm device, float32
+or bfloat16 (parameters and gradients independently), with fp32 moments in
+every case: a bf16 parameter is updated in fp32 and rounded back to
+nearest-even (no counterpart in the reference, whose kernel runs in the
+parameter's dtype, triton_adam.py:79-85).
 """
 
 from __future__ import annotations
@@ -30,10 +34,10 @@ import torch.nn as nn
 from .. import _lib
 
 
-def _check_tensor(t: torch.Tensor, name: str) -> None:
+def _check_tensor(t: torch.Tensor, name: str, bf16_ok: bool = False) -> None:
     _lib.require_gpu_tensor(t, name)
-    if t.dtype != torch.float32:
-        raise TypeError(f"{name} must be float32 (got {t.dtype})")
+    if t.dtype != torch.float32 and not (bf16_ok and t.dtype == torch.bfloat16):
+        raise TypeError(f"{name} must be float32{' or bfloat16' if bf16_ok else ''} (got {t.dtype})")
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
 
@@ -62,15 +66,16 @@ class _DevicePlan:
     def __init__(self, device: torch.device, entries: list[tuple[torch.Tensor, ...]]):
         lib = _lib.load()
         n = len(entries)
-        arr = (_lib.AdamWTensor * n)()
+        arr = (_lib.AdamWTensorEx * n)()
         for i, (p, g, m, v) in enumerate(entries):
-            arr[i] = _lib.AdamWTensor(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), p.numel())
+            flags = _lib.dtype_flag(p, _lib.BF16_PARAM, "param") | _lib.dtype_flag(g, _lib.BF16_GRAD, "param.grad")
+            arr[i] = _lib.AdamWTensorEx(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), p.numel(), flags, 0)
         nbytes = ctypes.c_size_t()
         _lib.check(lib.mamw_adamw_table_bytes(n, ctypes.byref(nbytes)), "mamw_adamw_table_bytes")
         host = torch.empty(max(nbytes.value, 1), dtype=torch.uint8)
         nblocks = ctypes.c_int64()
-        _lib.check(lib.mamw_adamw_table_pack(arr, n, host.data_ptr(), nbytes.value, ctypes.byref(nblocks)),
-                   "mamw_adamw_table_pack")
+        _lib.check(lib.mamw_adamw_table_pack_ex(arr, n, host.data_ptr(), nbytes.value, ctypes.byref(nblocks)),
+                   "mamw_adamw_table_pack_ex")
         self.device = device
         self.table = host.to(device)
         self.n_tensors = n
@@ -107,8 +112,8 @@ class HipAdamW:
         by_dev: dict[torch.device, list] = {}
         for p in active:
             g = p.grad
-            _check_tensor(p, "param")
-            _check_tensor(g, "param.grad")
+            _check_tensor(p, "param", bf16_ok=True)
+            _check_tensor(g, "param.grad", bf16_ok=True)
             if g.shape != p.shape or g.device != p.device:
                 raise ValueError("param.grad must match the parameter's shape and device")
             m, v = self.m[p], self.v[p]
@@ -124,7 +129,7 @@ class HipAdamW:
         active = [p for p in self.model_params if p.grad is not None]
         if not active:
             return
-        key = tuple((id(p), p.data_ptr(), p.grad.data_ptr()) for p in active)
+        key = tuple((id(p), p.data_ptr(), p.grad.data_ptr(), p.dtype, p.grad.dtype) for p in active)
         if key != self._plan_key:
             self._plan_key = None
             self._build_plans(active)

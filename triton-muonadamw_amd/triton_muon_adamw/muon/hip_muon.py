@@ -48,10 +48,10 @@ def scaled_lr(lr: float, adjust_lr_fn: str, rows: int, cols: int) -> float:
     return lr * math.sqrt(rows / cols)
 
 
-def _check_matrix(t: torch.Tensor, name: str, dtype=torch.float32) -> None:
+def _check_matrix(t: torch.Tensor, name: str, dtype=torch.float32, bf16_ok: bool = False) -> None:
     _lib.require_gpu_tensor(t, name)
-    if t.dtype != dtype:
-        raise TypeError(f"{name} must be {dtype} (got {t.dtype})")
+    if t.dtype != dtype and not (bf16_ok and t.dtype == torch.bfloat16):
+        raise TypeError(f"{name} must be {dtype}{' or torch.bfloat16' if bf16_ok else ''} (got {t.dtype})")
     if not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
 
@@ -239,7 +239,8 @@ class HipMuon:
         self.eps = eps
         self.momentum = {}
         for param in self.model_params:
-            self.momentum[param] = torch.zeros_like(param, device=param.device, dtype=param.dtype)
+            # fp32 state also for bf16 parameters (the reference uses the parameter's dtype, :407-412)
+            self.momentum[param] = torch.zeros_like(param, device=param.device, dtype=torch.float32)
         self._plan_key = None
         self._plan_lr = lr
         self._calls: list[_Call] = []
@@ -251,8 +252,8 @@ class HipMuon:
             if p.ndim != 2:
                 raise AssertionError("Muon only supports 2D tensors")
             g = p.grad
-            _check_matrix(p, "param")
-            _check_matrix(g, "param.grad")
+            _check_matrix(p, "param", bf16_ok=True)
+            _check_matrix(g, "param.grad", bf16_ok=True)
             if g.shape != p.shape or g.device != p.device:
                 raise ValueError("param.grad must match the parameter's shape and device")
             _check_matrix(self.momentum[p], "momentum")
@@ -277,8 +278,10 @@ class HipMuon:
                 arr = (_lib.MuonMatrix * len(chunk))()
                 for i, p in enumerate(chunk):
                     R, C = p.shape
+                    flags = (_lib.dtype_flag(p, _lib.BF16_PARAM, "param")
+                             | _lib.dtype_flag(p.grad, _lib.BF16_GRAD, "param.grad"))
                     arr[i] = _lib.MuonMatrix(p.data_ptr(), p.grad.data_ptr(), self.momentum[p].data_ptr(), None,
-                                             R, C, scaled_lr(self.lr, self.adjust_lr_fn, R, C), 0)
+                                             R, C, scaled_lr(self.lr, self.adjust_lr_fn, R, C), flags)
                 wsb = _workspace_bytes(len(chunk), m, n, self.steps)
                 calls.append(_Call(dev, arr, len(chunk), wsb, m, n))
                 need[dev] = max(need.get(dev, 0), wsb)
@@ -295,7 +298,8 @@ class HipMuon:
         active = [p for p in self.model_params if p.grad is not None]
         if not active:
             return
-        key = (self.adjust_lr_fn, self.steps, tuple((id(p), p.data_ptr(), p.grad.data_ptr()) for p in active))
+        key = (self.adjust_lr_fn, self.steps,
+               tuple((id(p), p.data_ptr(), p.grad.data_ptr(), p.dtype, p.grad.dtype) for p in active))
         if key != self._plan_key:
             self._plan_key = None
             self._build_calls(active)
