@@ -31,7 +31,7 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // Prep: one 64 x 64 tile of X (in X coordinates) per block.
 
 struct PrepArgs {
-    uint16_t* x;    // [batch][mp][np]
+    uint16_t* x;    // [batch][mp][np], k-blocked when xkb (see xoff)
     uint16_t* xt;   // [batch][np][mp]
     float* part;    // [batch][prep_tiles]
     int64_t mp, np;
@@ -39,7 +39,15 @@ struct PrepArgs {
     int tiles_j;    // np / 64
     float w_mom;    // 1 - beta   (lerp weight of the momentum update)
     float w_nest;   // beta       (lerp weight of the Nesterov blend)
+    int xkb;        // X is k-blocked
 };
+
+// Offset of X[r][c] in one matrix.  Row-major, or k-blocked: column panels of
+// 64 (the Gram's k step) stacked, each mp x 64 row-major, so one k step of a
+// 256-row tile panel is one contiguous 32 KB block.
+__device__ __forceinline__ int64_t xoff(int xkb, int64_t mp, int64_t np, int64_t r, int64_t c) {
+    return xkb ? (((c >> 6) * mp + r) << 6) + (c & 63) : r * np + c;
+}
 
 template <bool NESTEROV>
 __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs descs, const PrepArgs a) {
@@ -116,7 +124,7 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
             uint2 pk;
             pk.x = h[0] | (h[1] << 16);
             pk.y = h[2] | (h[3] << 16);
-            *reinterpret_cast<uint2*>(X + r * a.np + c) = pk;
+            *reinterpret_cast<uint2*>(X + xoff(a.xkb, a.mp, a.np, r, c)) = pk;
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) tileT[cg * 4 + e][rl] = uint16_t(h[e]);
@@ -132,7 +140,7 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
 #pragma unroll
         for (int k = 0; k < 8; ++k)
             w[k] = uint32_t(tileT[tr][seg + 2 * k]) | (uint32_t(tileT[tr][seg + 2 * k + 1]) << 16);
-        uint4* dst = reinterpret_cast<uint4*>(X + (c0 + tr) * a.np + r0 + seg);
+        uint4* dst = reinterpret_cast<uint4*>(X + xoff(a.xkb, a.mp, a.np, c0 + tr, r0 + seg));
         dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
         dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
     }
@@ -171,7 +179,7 @@ __global__ __launch_bounds__(256) void muon_scale_kernel(const PrepArgs a, const
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
         const int rl = rr + 16 * pass;
-        uint2* p = reinterpret_cast<uint2*>(X + (i0 + rl) * a.np + j0 + cg * 4);
+        uint2* p = reinterpret_cast<uint2*>(X + xoff(a.xkb, a.mp, a.np, i0 + rl, j0 + cg * 4));
         const uint2 v = *p;
         const uint32_t h[4] = {f32_to_bf16(bf16_to_f32(v.x & 0xffffu) * s), f32_to_bf16(bf16_to_f32(v.x >> 16) * s),
                                f32_to_bf16(bf16_to_f32(v.y & 0xffffu) * s), f32_to_bf16(bf16_to_f32(v.y >> 16) * s)};
@@ -197,7 +205,7 @@ __global__ __launch_bounds__(256) void muon_apply0_kernel(const MuonBatchDescs d
     const int64_t total = d.rows * d.cols;
     for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
         const int64_t r = e / d.cols, c = e % d.cols;
-        const float u = bf16_to_f32(d.tall ? X[c * a.np + r] : X[r * a.np + c]);
+        const float u = bf16_to_f32(d.tall ? X[xoff(a.xkb, a.mp, a.np, c, r)] : X[xoff(a.xkb, a.mp, a.np, r, c)]);
         if (d.flags & MAMW_BF16_PARAM) {
             uint16_t* ph = reinterpret_cast<uint16_t*>(d.param);
             ph[e] = uint16_t(f32_to_bf16(__builtin_fmaf(-d.slr, u, bf16_to_f32(ph[e]) * keep)));
@@ -245,6 +253,7 @@ struct GemmArgs {
     float beta;           // coefficient on src
     float keep;           // APPLY: 1 - lr * weight_decay
     int64_t m, n;         // APPLY: valid extent of X
+    int xkb;              // X k-blocked (xoff): the Gram's operands, the update's X output
 };
 
 // Launch block -> (matrix, tile row, tile col).
@@ -377,7 +386,7 @@ __device__ __forceinline__ void apply_chunk(const MuonMatDesc& d, uint4 w, int64
     }
 }
 
-template <int BM, int MODE>
+template <int BM, int MODE, bool KB>
 __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs g, const MuonBatchDescs descs) {
     constexpr int BN = BM;
     constexpr int WT = BM / 2;              // wave tile edge
@@ -396,17 +405,24 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     const int wm = wave >> 1, wn = wave & 1;
     int bat, ti, tj;
     decode_tile<SYM>(g, bat, ti, tj);
-    const uint16_t* Ag = g.aop + bat * g.a_bs + int64_t(ti) * BM * g.lda;
-    const uint16_t* Bg = g.bop + bat * g.b_bs + int64_t(tj) * BN * g.ldb;
-    // The tile's rows of each operand, up to column K of its last row.
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(Ag, ((BM - 1) * g.lda + g.K) * 2);
-    const __amdgpu_buffer_rsrc_t rb = make_rsrc(Bg, ((BN - 1) * g.ldb + g.K) * 2);
+    // Operand rows of the tile: row-major (row stride ld), or k-blocked (KB:
+    // Gram operands; row stride 64 inside a 64-wide panel, panel stride
+    // rows*64).  The buffer resource spans the tile's rows up to column K.
+    constexpr bool KBOP = KB && MODE == MODE_GRAM;
+    const int64_t rows_a = int64_t(g.tiles_m) * BM, rows_b = int64_t(g.tiles_n) * BN;
+    const uint16_t* Ag = g.aop + bat * g.a_bs + int64_t(ti) * BM * (KBOP ? 64 : g.lda);
+    const uint16_t* Bg = g.bop + bat * g.b_bs + int64_t(tj) * BN * (KBOP ? 64 : g.ldb);
+    const __amdgpu_buffer_rsrc_t ra =
+        make_rsrc(Ag, KBOP ? ((g.K / 64 - 1) * rows_a + BM) * 128 : ((BM - 1) * g.lda + g.K) * 2);
+    const __amdgpu_buffer_rsrc_t rb =
+        make_rsrc(Bg, KBOP ? ((g.K / 64 - 1) * rows_b + BN) * 128 : ((BN - 1) * g.ldb + g.K) * 2);
+    const int pa2 = int(rows_a) * 128, pb2 = int(rows_b) * 128;  // KBOP: bytes per k-step panel
 
     // Load i (0..LOADS-1) of an operand fills rows row0 = wave*BM/4 + 8i ..
     // row0+7: lane l lands at physical chunk l&7 of row row0 + l/8, which holds
     // logical chunk (l&7) ^ (l/8) ^ (i&1)  (lds_chunk with row0 a multiple of 8).
     const int lrow = lane >> 3;
-    const int lda2 = int(g.lda) * 2, ldb2 = int(g.ldb) * 2;
+    const int lda2 = KBOP ? 128 : int(g.lda) * 2, ldb2 = KBOP ? 128 : int(g.ldb) * 2;
     const int va0 = lrow * lda2 + (((lane & 7) ^ lrow) << 4), va1 = lrow * lda2 + (((lane & 7) ^ lrow ^ 1) << 4);
     const int vb0 = lrow * ldb2 + (((lane & 7) ^ lrow) << 4), vb1 = lrow * ldb2 + (((lane & 7) ^ lrow ^ 1) << 4);
     // DMA number i: operand A for i < LOADS, else B.
@@ -415,10 +431,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         uint16_t* dst = smem + buf * STAGE + (i < LOADS ? 0 : BM * kBK) + row0 * kBK;
         if (i < LOADS)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)dst, 16, (ii & 1) ? va1 : va0,
-                                                     row0 * lda2 + k0 * 2, 0, 0);
+                                                     row0 * lda2 + (KBOP ? (k0 >> 6) * pa2 : k0 * 2), 0, 0);
         else
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)dst, 16, (ii & 1) ? vb1 : vb0,
-                                                     row0 * ldb2 + k0 * 2, 0, 0);
+                                                     row0 * ldb2 + (KBOP ? (k0 >> 6) * pb2 : k0 * 2), 0, 0);
     };
     // Fragment read j of slice ks, in the order the MFMAs first use them
     // (a-major): fa0, fb0 .. fb[F-1], fa1 .. fa[F-1].
@@ -606,6 +622,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
             const int64_t orow = int64_t(ti) * BM + y, ocol = int64_t(tj) * BN + xc;
             if constexpr (MODE == MODE_APPLY) {
                 apply_chunk(d, wv, orow, ocol, orow < g.m ? int64_t(8) : int64_t(0), g.n - ocol, g.keep);
+            } else if constexpr (MODE == MODE_UPDATE && KB) {  // X k-blocked: tiles_m*BM rows, ldc columns
+                *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + xoff(1, int64_t(g.tiles_m) * BM, g.ldc, orow, ocol)) =
+                    wv;
             } else {
                 *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + orow * g.ldc + ocol) = wv;
             }
@@ -651,9 +670,18 @@ hipError_t launch_gemm(int tile, const GemmArgs& g, const MuonBatchDescs& d, int
     const int32_t kid = MODE == MODE_GRAM ? K_NS_GRAM : MODE == MODE_POLY ? K_NS_POLY
                       : MODE == MODE_UPDATE ? K_NS_UPDATE : K_NS_APPLY;
     const int32_t variant = tile;
+    if constexpr (MODE == MODE_GRAM || MODE == MODE_UPDATE) {
+        if (g.xkb) {
+            if (tile == 256)
+                return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, true>, grid, dim3(kGemmThreads), s,
+                              ga, d);
+            return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE, true>, grid, dim3(kGemmThreads), s,
+                          ga, d);
+        }
+    }
     if (tile == 256)
-        return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE>, grid, dim3(kGemmThreads), s, ga, d);
-    return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE>, grid, dim3(kGemmThreads), s, ga, d);
+        return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, false>, grid, dim3(kGemmThreads), s, ga, d);
+    return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE, false>, grid, dim3(kGemmThreads), s, ga, d);
 }
 
 GemmArgs gram_args(const uint16_t* X, uint16_t* A, int64_t mp, int64_t kp, int tile) {
@@ -762,6 +790,8 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
     pa.tiles_j = int(p.np / kPrepTile);
     pa.w_mom = float(1.0 - beta);
     pa.w_nest = float(beta);
+    // X k-blocked whenever a whole matrix's byte offsets fit the 31-bit buffer offsets.
+    pa.xkb = (p.mp * p.np * 2 < (int64_t(1) << 31)) ? 1 : 0;
     const double B = double(batch), m = double(p.m), n = double(p.n);
     dim3 pgrid(unsigned(p.prep_tiles), unsigned(batch));
     // prep: read grad, momentum; write momentum, X (4 + 4 + 4 + 2 bytes per element)
@@ -787,11 +817,14 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
     int cur = 0;
     for (int it = 0; it < ns_steps; ++it) {
         const bool last = (it == ns_steps - 1);
-        e = launch_gemm<MODE_GRAM>(p.tile, gram_args(X, A, p.mp, p.np, p.tile), descs, batch, f_gram, s);
+        GemmArgs gg = gram_args(X, A, p.mp, p.np, p.tile);
+        gg.xkb = pa.xkb;
+        e = launch_gemm<MODE_GRAM>(p.tile, gg, descs, batch, f_gram, s);
         if (e != hipSuccess) return int(e);
         e = launch_gemm<MODE_POLY>(p.tile, poly_args(A, Bm, p.mp, p.tile, b, c), descs, batch, f_poly, s);
         if (e != hipSuccess) return int(e);
         GemmArgs gu = update_args(Bm, XT[cur], X, last ? nullptr : XT[cur ^ 1], p.mp, p.np, p.tile, a);
+        gu.xkb = pa.xkb;
         if (last) {
             gu.keep = keep;
             gu.m = p.m;
