@@ -49,7 +49,7 @@ def kernel_label(name: str, variant: int) -> str:
     """Demangled template name of a GEMM launch as rocprofv3 reports it."""
     if name.startswith("ns_gemm_kernel:"):
         mode = name.split(":")[1]
-        return f"ns_gemm_kernel<{variant}, {MODE_NUM[mode]}>"
+        return f"ns_gemm_kernel<{variant // 2}, {MODE_NUM[mode]}, {'true' if variant % 2 else 'false'}>"
     return name
 
 

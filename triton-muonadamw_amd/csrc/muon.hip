@@ -669,9 +669,10 @@ hipError_t launch_gemm(int tile, const GemmArgs& g, const MuonBatchDescs& d, int
     dim3 grid(unsigned(ga.tiles_per_matrix) * unsigned(batch));
     const int32_t kid = MODE == MODE_GRAM ? K_NS_GRAM : MODE == MODE_POLY ? K_NS_POLY
                       : MODE == MODE_UPDATE ? K_NS_UPDATE : K_NS_APPLY;
-    const int32_t variant = tile;
+    const bool kb = (MODE == MODE_GRAM || MODE == MODE_UPDATE) && g.xkb;
+    const int32_t variant = 2 * tile + (kb ? 1 : 0);  // tile and the KB template flag
     if constexpr (MODE == MODE_GRAM || MODE == MODE_UPDATE) {
-        if (g.xkb) {
+        if (kb) {
             if (tile == 256)
                 return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, true>, grid, dim3(kGemmThreads), s,
                               ga, d);
