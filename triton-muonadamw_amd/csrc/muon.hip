@@ -26,6 +26,16 @@ constexpr int kBK = 64;
 enum GemmMode { MODE_GRAM = 0, MODE_POLY = 1, MODE_UPDATE = 2, MODE_APPLY = 3 };
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t* lds_i16x4_ptr_t;
+
+// gfx950 LDS transpose read (ds_read_b64_tr_b16) of 16-bit elements: within
+// each group of 16 lanes, lane j names 4 consecutive elements c_j[0..3];
+// lane i receives c_{4r + i/4}[i%4] for r = 0..3.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+    const i16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_ptr_t)(lds_ptr_t)(p));
+    return __builtin_bit_cast(uint2, v);
+}
 
 // ---------------------------------------------------------------------------
 // Prep: one 64 x 64 tile of X (in X coordinates) per block.
@@ -113,17 +123,14 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
                 }
             }
         }
-        uint32_t h[4];
+        const uint2 pk = make_uint2(pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3]));
+        const uint32_t h[4] = {pk.x & 0xffffu, pk.x >> 16, pk.y & 0xffffu, pk.y >> 16};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            h[e] = f32_to_bf16(u[e]);
             const float xb = bf16_to_f32(h[e]);
             ss += xb * xb;
         }
         if (!tall) {  // X = bf16(u): parameter rows are X rows
-            uint2 pk;
-            pk.x = h[0] | (h[1] << 16);
-            pk.y = h[2] | (h[3] << 16);
             *reinterpret_cast<uint2*>(X + xoff(a.xkb, a.mp, a.np, r, c)) = pk;
         } else {
 #pragma unroll
@@ -181,11 +188,13 @@ __global__ __launch_bounds__(256) void muon_scale_kernel(const PrepArgs a, const
         const int rl = rr + 16 * pass;
         uint2* p = reinterpret_cast<uint2*>(X + xoff(a.xkb, a.mp, a.np, i0 + rl, j0 + cg * 4));
         const uint2 v = *p;
-        const uint32_t h[4] = {f32_to_bf16(bf16_to_f32(v.x & 0xffffu) * s), f32_to_bf16(bf16_to_f32(v.x >> 16) * s),
-                               f32_to_bf16(bf16_to_f32(v.y & 0xffffu) * s), f32_to_bf16(bf16_to_f32(v.y >> 16) * s)};
-        *p = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-#pragma unroll
-        for (int e = 0; e < 4; ++e) tileT[cg * 4 + e][rl] = uint16_t(h[e]);
+        const uint2 w = make_uint2(pack_bf16x2(bf16_to_f32(v.x & 0xffffu) * s, bf16_to_f32(v.x >> 16) * s),
+                                   pack_bf16x2(bf16_to_f32(v.y & 0xffffu) * s, bf16_to_f32(v.y >> 16) * s));
+        *p = w;
+        tileT[cg * 4 + 0][rl] = uint16_t(w.x);
+        tileT[cg * 4 + 1][rl] = uint16_t(w.x >> 16);
+        tileT[cg * 4 + 2][rl] = uint16_t(w.y);
+        tileT[cg * 4 + 3][rl] = uint16_t(w.y >> 16);
     }
     __syncthreads();
     const int tr = tid >> 2, seg = (tid & 3) * 16;
@@ -565,10 +574,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
                         v[e] = MODE == MODE_POLY ? __builtin_fmaf(g.alpha, v[e], g.beta * sv[e])
                                                  : __builtin_fmaf(g.beta, sv[e], v[e]);
                 }
-                uint32_t h[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) h[e] = f32_to_bf16(v[e]);
-                *cell = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+                *cell = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
             }
         }
     }
@@ -611,14 +617,22 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     // Direct orientation, gathered from TT columns: row (ti*BM + y) of the
     // output holds TT[x][y] over x.  Symmetric products: the tile's own block
     // (off the diagonal); UPDATE: X; APPLY: the parameter of a wide matrix.
+    // Two transpose reads give a lane 8 consecutive columns of one row: in a
+    // 16-lane group, lane j names TT[xc + j/4][yb + 4(j%4) ..], so lane i
+    // receives C[yb + i][xc .. xc+3] (and xc+4 .. xc+7 from the second read).
+    // A group covers 16 rows x 8 columns, the 4 groups of a wave adjacent
+    // 8-column pieces of the same rows (2-way LDS bank conflicts at most).
     if ((SYM && !diag) || MODE == MODE_UPDATE || (MODE == MODE_APPLY && !tall)) {
-        for (int k = tid; k < BM * (BN / 8); k += kGemmThreads) {
-            const int y = k / (BN / 8), xc = (k % (BN / 8)) * 8;
-            uint32_t w[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                w[j] = uint32_t(TT[tt(xc + 2 * j, y)]) | (uint32_t(TT[tt(xc + 2 * j + 1, y)]) << 16);
-            const uint4 wv = make_uint4(w[0], w[1], w[2], w[3]);
+        constexpr int NXQ = BN / 32;                // 32-column pieces of a 16-row band
+        constexpr int NIT = (BM / 16) * NXQ / 4;    // per wave
+        const int gi = lane & 15, grp = lane >> 4;
+        for (int it = 0; it < NIT; ++it) {
+            const int t = it * 4 + wave;
+            const int yb = (t / NXQ) * 16, xc = (t % NXQ) * 32 + grp * 8;
+            const int xr = xc + (gi >> 2), yr = yb + 4 * (gi & 3);
+            const uint2 lo = lds_read_tr16(TT + tt(xr, yr)), hi = lds_read_tr16(TT + tt(xr + 4, yr));
+            const uint4 wv = make_uint4(lo.x, lo.y, hi.x, hi.y);
+            const int y = yb + gi;
             const int64_t orow = int64_t(ti) * BM + y, ocol = int64_t(tj) * BN + xc;
             if constexpr (MODE == MODE_APPLY) {
                 apply_chunk(d, wv, orow, ocol, orow < g.m ? int64_t(8) : int64_t(0), g.n - ocol, g.keep);
