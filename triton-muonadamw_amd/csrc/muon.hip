@@ -471,8 +471,34 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     // One slice: MFMAs on (ca, cb); reads of the next slice into (na, nb) when
     // `reads`; the DMA of step k0/kBK into buffer lbuf when `loads`.  All flags
     // are compile-time constants at every call, so the body has no branches.
+    // Epilogue coefficient tile (POLY: A; UPDATE/APPLY: X^T), stored
+    // transposed in LDS as TT[x][y] = src[(tj*BN + x) * lds + ti*BM + y] (A is
+    // symmetric; X^T holds X transposed), in 1-KB DMA blocks: block b fills TT
+    // rows b*RPI .. b*RPI+RPI-1.  TT row x holds 16-byte chunks of BM/8 y
+    // values, logical chunk c at physical chunk c ^ (x ^ x>>3) (mod BM/8).
+    constexpr int NCH = BM / 8;                   // 16-byte chunks per TT row
+    constexpr int RPI = 64 / NCH;                 // TT rows per 1-KB block
+    constexpr int NSB = BN / RPI;                 // blocks of the whole tile
+    constexpr int NPRE = STAGE * 2 / 1024;        // blocks in stage buffer 0 (all of TT when BM = 128)
+    static_assert(NPRE == 8 * LOADS && NPRE <= NSB, "prefetch blocks map onto the DMA slots of one step");
+    const uint16_t* S = MODE == MODE_GRAM ? g.aop  // (unused)
+                                          : g.src + bat * g.src_bs + int64_t(tj) * BN * g.lds + int64_t(ti) * BM;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(S, MODE == MODE_GRAM ? 0 : ((BN - 1) * g.lds + BM) * 2);
+    const int lds2 = MODE == MODE_GRAM ? 0 : int(g.lds) * 2;
+    auto src_load = [&](int b) {
+        const int x0 = b * RPI, x = x0 + lane / NCH;
+        const int c = ((lane % NCH) ^ x ^ (x >> 3)) & (NCH - 1);  // logical chunk at physical lane % NCH
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(smem + x0 * BM), 16, (lane / NCH) * lds2 + c * 16,
+                                                 x0 * lds2, 0, 0);
+    };
+
+    // One slice: MFMAs on (ca, cb); reads of the next slice into (na, nb) when
+    // `reads`; per `loads`, the DMA of step k0/kBK into buffer lbuf (1) or this
+    // wave's share of the coefficient blocks that fit in stage buffer 0 (2).
+    // All flags are compile-time constants at every call, so the body has no
+    // branches.
     auto slice = [&](const bf16x8_t (&ca)[F], const bf16x8_t (&cb)[F], bf16x8_t (&na)[F], bf16x8_t (&nb)[F],
-                     bool reads, int rbuf, int rks, bool loads, int k0, int lbuf) {
+                     bool reads, int rbuf, int rks, int loads, int k0, int lbuf) {
 #pragma unroll
         for (int i = 0; i < NMF; ++i) {
             acc[i / F][i % F] =
@@ -481,8 +507,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
             for (int r = 0; r < RPM; ++r)
                 if (reads && i * RPM + r < 2 * F) read1(na, nb, rbuf, rks, i * RPM + r);
 #pragma unroll
-            for (int l = 0; l < LPM; ++l)
-                if (loads && i * LPM + l < 2 * LOADS) load1(i * LPM + l, k0, lbuf);
+            for (int l = 0; l < LPM; ++l) {
+                if (loads == 1 && i * LPM + l < 2 * LOADS) load1(i * LPM + l, k0, lbuf);
+                if (loads == 2 && i * LPM + l < 2 * LOADS) src_load(wave * 2 * LOADS + i * LPM + l);
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
@@ -499,25 +527,47 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     bf16x8_t fa0[F], fb0[F], fa1[F], fb1[F];
 #pragma unroll
     for (int j = 0; j < 2 * F; ++j) read1(fa0, fb0, 0, 0, j);
-    // Steps 0..KT-2.  Before the barrier this wave's loads of step kt+1 and its
+    // Before the barrier of step kt this wave's loads of step kt+1 and its
     // reads of the last slice are complete; after it everyone's are, so buffer
-    // `buf` takes step kt+2 (the last step again when kt+2 == KT, into a buffer
-    // nothing reads any more, which keeps the loop free of branches).
-    for (int kt = 0; kt < KT - 1; ++kt) {
-        const int buf = kt & 1;
-        slice(fa0, fb0, fa1, fb1, true, buf, 1, false, 0, 0);
-        slice(fa1, fb1, fa0, fb0, true, buf, 2, false, 0, 0);
-        slice(fa0, fb0, fa1, fb1, true, buf, 3, false, 0, 0);
+    // `buf` takes step kt+2.
+    if constexpr (MODE == MODE_GRAM) {
+        // Steps 0..KT-2; step KT-2 loads the last step again, into a buffer
+        // nothing reads any more (keeps the loop free of branches).
+        for (int kt = 0; kt < KT - 1; ++kt) {
+            const int buf = kt & 1;
+            slice(fa0, fb0, fa1, fb1, true, buf, 1, 0, 0, 0);
+            slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0);
+            slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0);
+            __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+            asm volatile("s_barrier" ::: "memory");
+            slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, min(kt + 2, KT - 1) * kBK, buf);
+        }
+    } else {
+        // Steps 0..KT-3, then step KT-2 (K is a multiple of 2 kBK: buffer 0).
+        // Once step KT-2 releases buffer 0, it takes the first NPRE blocks of
+        // the coefficient tile while step KT-1 runs from buffer 1.
+        for (int kt = 0; kt < KT - 2; ++kt) {
+            const int buf = kt & 1;
+            slice(fa0, fb0, fa1, fb1, true, buf, 1, 0, 0, 0);
+            slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0);
+            slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0);
+            __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+            asm volatile("s_barrier" ::: "memory");
+            slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, (kt + 2) * kBK, buf);
+        }
+        slice(fa0, fb0, fa1, fb1, true, 0, 1, 0, 0, 0);
+        slice(fa1, fb1, fa0, fb0, true, 0, 2, 0, 0, 0);
+        slice(fa0, fb0, fa1, fb1, true, 0, 3, 0, 0, 0);
         __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
         asm volatile("s_barrier" ::: "memory");
-        slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, true, min(kt + 2, KT - 1) * kBK, buf);
+        slice(fa1, fb1, fa0, fb0, true, 1, 0, 2, 0, 0);
     }
     {
         const int buf = (KT - 1) & 1;
-        slice(fa0, fb0, fa1, fb1, true, buf, 1, false, 0, 0);
-        slice(fa1, fb1, fa0, fb0, true, buf, 2, false, 0, 0);
-        slice(fa0, fb0, fa1, fb1, true, buf, 3, false, 0, 0);
-        slice(fa1, fb1, fa0, fb0, false, 0, 0, false, 0, 0);
+        slice(fa0, fb0, fa1, fb1, true, buf, 1, 0, 0, 0);
+        slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0);
+        slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0);
+        slice(fa1, fb1, fa0, fb0, false, 0, 0, 0, 0, 0);
     }
     __builtin_amdgcn_s_waitcnt(0x0070);  // no DMA outlives the loop
 
@@ -527,26 +577,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     // at physical chunk c ^ (x ^ x>>3) (mod chunks per row).  That spreads both
     // a lane's 4 rows of one column and 8 columns gathered at one row over the
     // banks (at most 2-way).
-    constexpr int NCH = BM / 8;  // 16-byte chunks per TT row
     uint16_t* const TT = smem;   // BN rows x BM bf16 (fits in the two stages)
     auto tt = [&](int x, int y) { return x * BM + ((((y >> 3) ^ x ^ (x >> 3)) & (NCH - 1)) << 3) + (y & 7); };
     const bool diag = SYM && ti == tj;
     __syncthreads();  // every wave is done with the stage buffers
 
     if constexpr (MODE != MODE_GRAM) {
-        // Coefficient operand, TT[x][y] = src[(tj*BN + x) * lds + ti*BM + y]:
-        // A is symmetric (A[r][col] = A[col][r]); X^T holds X transposed.
-        const uint16_t* S = g.src + bat * g.src_bs + int64_t(tj) * BN * g.lds + int64_t(ti) * BM;
-        const __amdgpu_buffer_rsrc_t rs = make_rsrc(S, ((BN - 1) * g.lds + BM) * 2);
-        constexpr int RPI = 64 / NCH;        // TT rows per 1-KB load
-        constexpr int NLD = BN / RPI / 4;    // loads per wave
-        const int lds2 = int(g.lds) * 2;
-        for (int i = 0; i < NLD; ++i) {
-            const int x0 = (wave * NLD + i) * RPI, x = x0 + lane / NCH;
-            const int c = ((lane % NCH) ^ x ^ (x >> 3)) & (NCH - 1);  // logical chunk at physical lane % NCH
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(TT + x0 * BM), 16, (lane / NCH) * lds2 + c * 16,
-                                                     x0 * lds2, 0, 0);
-        }
+        // The rest of the coefficient tile (the blocks in stage buffer 1).
+        constexpr int NREST = (NSB - NPRE) / 4;  // per wave
+#pragma unroll
+        for (int i = 0; i < NREST; ++i) src_load(NPRE + wave * NREST + i);
         __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
         __syncthreads();
     }
@@ -677,6 +717,9 @@ __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __r
 template <int MODE>
 hipError_t launch_gemm(int tile, const GemmArgs& g, const MuonBatchDescs& d, int batch, double flops,
                        hipStream_t s) {
+    // Products with an epilogue coefficient peel the last two k steps and
+    // prefetch into stage buffer 0 during the last one: K is a multiple of 2 kBK.
+    if (g.K < kBK || g.K % kBK != 0 || (MODE != MODE_GRAM && g.K % (2 * kBK) != 0)) return hipErrorInvalidValue;
     GemmArgs ga = g;
     ga.tiles_per_matrix = (MODE == MODE_GRAM || MODE == MODE_POLY) ? g.tiles_m * (g.tiles_m + 1) / 2
                                                                    : g.tiles_m * g.tiles_n;
