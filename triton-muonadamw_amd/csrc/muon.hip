@@ -42,21 +42,23 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
 
 struct PrepArgs {
     uint16_t* x;    // [batch][mp][np], k-blocked when xkb (see xoff)
-    uint16_t* xt;   // [batch][np][mp]
+    uint16_t* xt;   // [batch][np][mp], k-blocked when xkb
     float* part;    // [batch][prep_tiles]
     int64_t mp, np;
     int64_t prep_tiles;
     int tiles_j;    // np / 64
     float w_mom;    // 1 - beta   (lerp weight of the momentum update)
     float w_nest;   // beta       (lerp weight of the Nesterov blend)
-    int xkb;        // X is k-blocked
+    int xkb;        // workspace matrices are k-blocked
 };
 
-// Offset of X[r][c] in one matrix.  Row-major, or k-blocked: column panels of
-// 64 (the Gram's k step) stacked, each mp x 64 row-major, so one k step of a
-// 256-row tile panel is one contiguous 32 KB block.
-__device__ __forceinline__ int64_t xoff(int xkb, int64_t mp, int64_t np, int64_t r, int64_t c) {
-    return xkb ? (((c >> 6) * mp + r) << 6) + (c & 63) : r * np + c;
+// Offset of element [r][c] of a rows x cols workspace matrix (X: mp x np,
+// X^T: np x mp, A and B: mp x mp).  Row-major, or k-blocked: column panels of
+// 64 (one GEMM k step) stacked, each rows x 64 row-major, so one k step of a
+// 256-row operand tile is one contiguous 32 KB block and a 256 x 256 output
+// tile is four contiguous 32 KB blocks.
+__device__ __forceinline__ int64_t xoff(int xkb, int64_t rows, int64_t cols, int64_t r, int64_t c) {
+    return xkb ? (((c >> 6) * rows + r) << 6) + (c & 63) : r * cols + c;
 }
 
 template <bool NESTEROV>
@@ -201,7 +203,7 @@ __global__ __launch_bounds__(256) void muon_scale_kernel(const PrepArgs a, const
     uint32_t w[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) w[k] = uint32_t(tileT[tr][seg + 2 * k]) | (uint32_t(tileT[tr][seg + 2 * k + 1]) << 16);
-    uint4* dst = reinterpret_cast<uint4*>(XT + (j0 + tr) * a.mp + i0 + seg);
+    uint4* dst = reinterpret_cast<uint4*>(XT + xoff(a.xkb, a.np, a.mp, j0 + tr, i0 + seg));
     dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
     dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
 }
@@ -235,12 +237,16 @@ __global__ __launch_bounds__(256) void muon_apply0_kernel(const MuonBatchDescs d
 // per operand tile, so a lane needs a single 32-bit offset per operand).
 //
 // A step is four 16-wide k slices of NMF MFMAs each.  Every slice issues its
-// MFMAs one at a time with the next slice's fragment reads, and in the last
-// slice the DMA of the step after next, woven in between (sched_barrier keeps
-// that order), so the matrix pipe never waits for an address computation or a
-// burst of loads.  The block barrier sits before the last slice: the MFMAs of
-// that slice run from registers while the barrier releases the buffer just
-// read, and the next step's first fragments are read under them.  LDS rows
+// MFMAs one at a time with the next slice's fragment reads woven in between
+// (sched_barrier keeps that order), so the matrix pipe never waits for an
+// address computation.  The DMA of a step is split in two halves: the first
+// goes out in the last slice of the step two ahead, the second in the first
+// slice of the next step, one load per two MFMAs.  Spreading the loads keeps
+// the per-CU queue of outstanding L2 requests busy without the load issue
+// stalling the MFMAs behind it (one 16-load burst per step measured 5-9%
+// slower).  The block barrier sits before the last slice: the MFMAs of that
+// slice run from registers while the barrier releases the buffer just read,
+// and the next step's first fragments are read under them.  LDS rows
 // are 128 bytes with the 16-byte chunk index XOR-swizzled (lds_chunk), so
 // fragment reads are bank-conflict free.
 
@@ -262,7 +268,7 @@ struct GemmArgs {
     float beta;           // coefficient on src
     float keep;           // APPLY: 1 - lr * weight_decay
     int64_t m, n;         // APPLY: valid extent of X
-    int xkb;              // X k-blocked (xoff): the Gram's operands, the update's X output
+    int xkb;              // operands, coefficient and outputs k-blocked (xoff)
 };
 
 // Launch block -> (matrix, tile row, tile col).
@@ -403,7 +409,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     constexpr int NMF = F * F;              // MFMAs per 16-wide k slice
     constexpr int LOADS = BM / 32;          // DMA loads per wave per operand per step (8 rows each)
     constexpr int RPM = (2 * F + NMF - 1) / NMF;      // fragment reads woven in per MFMA
-    constexpr int LPM = (2 * LOADS + NMF - 1) / NMF;  // DMA loads woven in per MFMA
+    constexpr int LPM = (2 * LOADS + NMF - 1) / NMF;  // coefficient-tile DMA loads woven in per MFMA
     constexpr int STAGE = (BM + BN) * kBK;  // bf16 elements per LDS stage
     constexpr bool SYM = (MODE == MODE_GRAM || MODE == MODE_POLY);
     __shared__ uint4 smem_v[2 * STAGE / 8];
@@ -415,9 +421,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     int bat, ti, tj;
     decode_tile<SYM>(g, bat, ti, tj);
     // Operand rows of the tile: row-major (row stride ld), or k-blocked (KB:
-    // Gram operands; row stride 64 inside a 64-wide panel, panel stride
-    // rows*64).  The buffer resource spans the tile's rows up to column K.
-    constexpr bool KBOP = KB && MODE == MODE_GRAM;
+    // row stride 64 inside a 64-wide panel, panel stride rows*64).  The buffer
+    // resource spans the tile's rows up to column K.
+    constexpr bool KBOP = KB;
     const int64_t rows_a = int64_t(g.tiles_m) * BM, rows_b = int64_t(g.tiles_n) * BN;
     const uint16_t* Ag = g.aop + bat * g.a_bs + int64_t(ti) * BM * (KBOP ? 64 : g.lda);
     const uint16_t* Bg = g.bop + bat * g.b_bs + int64_t(tj) * BN * (KBOP ? 64 : g.ldb);
@@ -481,24 +487,32 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     constexpr int NSB = BN / RPI;                 // blocks of the whole tile
     constexpr int NPRE = STAGE * 2 / 1024;        // blocks in stage buffer 0 (all of TT when BM = 128)
     static_assert(NPRE == 8 * LOADS && NPRE <= NSB, "prefetch blocks map onto the DMA slots of one step");
+    // Rows of the coefficient matrix and of the transposed-orientation output
+    // (A or B: mp; X^T: np), which address their k-blocked panels.
+    const int64_t rows_t = int64_t(g.tiles_n) * BN;
     const uint16_t* S = MODE == MODE_GRAM ? g.aop  // (unused)
-                                          : g.src + bat * g.src_bs + int64_t(tj) * BN * g.lds + int64_t(ti) * BM;
-    const __amdgpu_buffer_rsrc_t rs = make_rsrc(S, MODE == MODE_GRAM ? 0 : ((BN - 1) * g.lds + BM) * 2);
-    const int lds2 = MODE == MODE_GRAM ? 0 : int(g.lds) * 2;
+                      : KB ? g.src + bat * g.src_bs + (int64_t(ti) * (BM / 64) * rows_t + int64_t(tj) * BN) * 64
+                           : g.src + bat * g.src_bs + int64_t(tj) * BN * g.lds + int64_t(ti) * BM;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(S, MODE == MODE_GRAM ? 0
+                                                   : KB ? ((BM / 64 - 1) * rows_t + BN) * 128
+                                                        : ((BN - 1) * g.lds + BM) * 2);
+    const int lds2 = MODE == MODE_GRAM ? 0 : KB ? 128 : int(g.lds) * 2;  // bytes between TT rows' sources
+    const int pnl2 = int(rows_t) * 128;                                   // KB: bytes per 64-column panel
     auto src_load = [&](int b) {
         const int x0 = b * RPI, x = x0 + lane / NCH;
         const int c = ((lane % NCH) ^ x ^ (x >> 3)) & (NCH - 1);  // logical chunk at physical lane % NCH
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(smem + x0 * BM), 16, (lane / NCH) * lds2 + c * 16,
+        const int coff = KB ? (c >> 3) * pnl2 + (c & 7) * 16 : c * 16;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(smem + x0 * BM), 16, (lane / NCH) * lds2 + coff,
                                                  x0 * lds2, 0, 0);
     };
 
     // One slice: MFMAs on (ca, cb); reads of the next slice into (na, nb) when
-    // `reads`; per `loads`, the DMA of step k0/kBK into buffer lbuf (1) or this
-    // wave's share of the coefficient blocks that fit in stage buffer 0 (2).
-    // All flags are compile-time constants at every call, so the body has no
-    // branches.
+    // `reads`; per `loads`, DMA loads [llo, lhi) of step k0/kBK into buffer
+    // lbuf (1) or this wave's share of the coefficient blocks that fit in stage
+    // buffer 0 (2).  All arguments are compile-time constants at every call, so
+    // the body has no branches.
     auto slice = [&](const bf16x8_t (&ca)[F], const bf16x8_t (&cb)[F], bf16x8_t (&na)[F], bf16x8_t (&nb)[F],
-                     bool reads, int rbuf, int rks, int loads, int k0, int lbuf) {
+                     bool reads, int rbuf, int rks, int loads, int k0, int lbuf, int llo, int lhi) {
 #pragma unroll
         for (int i = 0; i < NMF; ++i) {
             acc[i / F][i % F] =
@@ -507,40 +521,47 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
             for (int r = 0; r < RPM; ++r)
                 if (reads && i * RPM + r < 2 * F) read1(na, nb, rbuf, rks, i * RPM + r);
 #pragma unroll
-            for (int l = 0; l < LPM; ++l) {
-                if (loads == 1 && i * LPM + l < 2 * LOADS) load1(i * LPM + l, k0, lbuf);
+            for (int l = 0; l < LPM; ++l)
                 if (loads == 2 && i * LPM + l < 2 * LOADS) src_load(wave * 2 * LOADS + i * LPM + l);
+            if (loads == 1) {
+                const int nl = lhi - llo, j0 = llo + (i * nl) / NMF, j1 = llo + ((i + 1) * nl) / NMF;
+#pragma unroll
+                for (int j = j0; j < j1; ++j) load1(j, k0, lbuf);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
 
     const int KT = g.K / kBK;
+    constexpr int NL = 2 * LOADS, LH = LOADS;  // DMA loads per step; the half issued two steps ahead
 #pragma unroll
-    for (int i = 0; i < 2 * LOADS; ++i) load1(i, 0, 0);
+    for (int i = 0; i < NL; ++i) load1(i, 0, 0);
     __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
     asm volatile("s_barrier" ::: "memory");
     if (KT > 1) {
 #pragma unroll
-        for (int i = 0; i < 2 * LOADS; ++i) load1(i, kBK, 1);
+        for (int i = 0; i < LH; ++i) load1(i, kBK, 1);
     }
     bf16x8_t fa0[F], fb0[F], fa1[F], fb1[F];
 #pragma unroll
     for (int j = 0; j < 2 * F; ++j) read1(fa0, fb0, 0, 0, j);
-    // Before the barrier of step kt this wave's loads of step kt+1 and its
-    // reads of the last slice are complete; after it everyone's are, so buffer
-    // `buf` takes step kt+2.
+    // Step kt reads buffer kt&1.  Buffer kt&1 ^ 1 has been free since the
+    // barrier of step kt-1, whose last slice started the first half of step
+    // kt+1 there; the first slice of step kt adds the second half.  Before the
+    // barrier of step kt this wave's loads of step kt+1 and its reads of the
+    // step are complete; after it everyone's are, so buffer kt&1 takes the
+    // first half of step kt+2.
     if constexpr (MODE == MODE_GRAM) {
-        // Steps 0..KT-2; step KT-2 loads the last step again, into a buffer
-        // nothing reads any more (keeps the loop free of branches).
+        // Steps 0..KT-2; step KT-2 loads the first half of the last step again,
+        // into a buffer nothing reads any more (keeps the loop free of branches).
         for (int kt = 0; kt < KT - 1; ++kt) {
             const int buf = kt & 1;
-            slice(fa0, fb0, fa1, fb1, true, buf, 1, 0, 0, 0);
-            slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0);
-            slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0);
+            slice(fa0, fb0, fa1, fb1, true, buf, 1, 1, (kt + 1) * kBK, buf ^ 1, LH, NL);
+            slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0, 0, 0);
+            slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0, 0, 0);
             __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
             asm volatile("s_barrier" ::: "memory");
-            slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, min(kt + 2, KT - 1) * kBK, buf);
+            slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, min(kt + 2, KT - 1) * kBK, buf, 0, LH);
         }
     } else {
         // Steps 0..KT-3, then step KT-2 (K is a multiple of 2 kBK: buffer 0).
@@ -548,26 +569,26 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         // the coefficient tile while step KT-1 runs from buffer 1.
         for (int kt = 0; kt < KT - 2; ++kt) {
             const int buf = kt & 1;
-            slice(fa0, fb0, fa1, fb1, true, buf, 1, 0, 0, 0);
-            slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0);
-            slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0);
+            slice(fa0, fb0, fa1, fb1, true, buf, 1, 1, (kt + 1) * kBK, buf ^ 1, LH, NL);
+            slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0, 0, 0);
+            slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0, 0, 0);
             __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
             asm volatile("s_barrier" ::: "memory");
-            slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, (kt + 2) * kBK, buf);
+            slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, (kt + 2) * kBK, buf, 0, LH);
         }
-        slice(fa0, fb0, fa1, fb1, true, 0, 1, 0, 0, 0);
-        slice(fa1, fb1, fa0, fb0, true, 0, 2, 0, 0, 0);
-        slice(fa0, fb0, fa1, fb1, true, 0, 3, 0, 0, 0);
+        slice(fa0, fb0, fa1, fb1, true, 0, 1, 1, (KT - 1) * kBK, 1, LH, NL);
+        slice(fa1, fb1, fa0, fb0, true, 0, 2, 0, 0, 0, 0, 0);
+        slice(fa0, fb0, fa1, fb1, true, 0, 3, 0, 0, 0, 0, 0);
         __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
         asm volatile("s_barrier" ::: "memory");
-        slice(fa1, fb1, fa0, fb0, true, 1, 0, 2, 0, 0);
+        slice(fa1, fb1, fa0, fb0, true, 1, 0, 2, 0, 0, 0, 0);
     }
     {
         const int buf = (KT - 1) & 1;
-        slice(fa0, fb0, fa1, fb1, true, buf, 1, 0, 0, 0);
-        slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0);
-        slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0);
-        slice(fa1, fb1, fa0, fb0, false, 0, 0, 0, 0, 0);
+        slice(fa0, fb0, fa1, fb1, true, buf, 1, 0, 0, 0, 0, 0);
+        slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0, 0, 0);
+        slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0, 0, 0);
+        slice(fa1, fb1, fa0, fb0, false, 0, 0, 0, 0, 0, 0, 0);
     }
     __builtin_amdgcn_s_waitcnt(0x0070);  // no DMA outlives the loop
 
@@ -641,16 +662,23 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     const MuonMatDesc& d = descs.d[bat];
     const bool tall = MODE == MODE_APPLY && d.tall;
     if (SYM || (MODE == MODE_UPDATE && g.ct) || tall) {
-        for (int k = tid; k < BN * NCH; k += kGemmThreads) {
-            const int x = k / NCH, c = k % NCH;
+        // k-blocked outputs: each wave writes 8 rows x 128 bytes of one panel
+        // (one contiguous KB); otherwise 2 rows x 32 chunks.
+        constexpr bool PANEL = KB && MODE != MODE_APPLY;
+#pragma unroll 8
+        for (int it = 0; it < BN * NCH / kGemmThreads; ++it) {
+            const int k = it * kGemmThreads + tid;
+            const int x = PANEL ? (k >> 3) % BN : k / NCH;
+            const int c = PANEL ? ((k >> 3) / BN) * 8 + (k & 7) : k % NCH;
             const uint4 w = *reinterpret_cast<const uint4*>(TT + x * BM + (((c ^ x ^ (x >> 3)) & (NCH - 1)) << 3));
             const int64_t orow = int64_t(tj) * BN + x, ocol = int64_t(ti) * BM + c * 8;
             if constexpr (MODE == MODE_APPLY) {
                 apply_chunk(d, w, orow, ocol, orow < g.n ? int64_t(8) : int64_t(0), g.m - ocol, g.keep);
             } else if constexpr (SYM) {
-                *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + orow * g.ldc + ocol) = w;
+                *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + (KB ? xoff(1, rows_t, 0, orow, ocol) : orow * g.ldc + ocol)) = w;
             } else {
-                *reinterpret_cast<uint4*>(g.ct + bat * g.ct_bs + orow * g.ldct + ocol) = w;
+                *reinterpret_cast<uint4*>(g.ct + bat * g.ct_bs + (KB ? xoff(1, rows_t, 0, orow, ocol) : orow * g.ldct + ocol)) =
+                    w;
             }
         }
     }
@@ -666,6 +694,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         constexpr int NXQ = BN / 32;                // 32-column pieces of a 16-row band
         constexpr int NIT = (BM / 16) * NXQ / 4;    // per wave
         const int gi = lane & 15, grp = lane >> 4;
+#pragma unroll 4
         for (int it = 0; it < NIT; ++it) {
             const int t = it * 4 + wave;
             const int yb = (t / NXQ) * 16, xc = (t % NXQ) * 32 + grp * 8;
@@ -676,9 +705,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
             const int64_t orow = int64_t(ti) * BM + y, ocol = int64_t(tj) * BN + xc;
             if constexpr (MODE == MODE_APPLY) {
                 apply_chunk(d, wv, orow, ocol, orow < g.m ? int64_t(8) : int64_t(0), g.n - ocol, g.keep);
-            } else if constexpr (MODE == MODE_UPDATE && KB) {  // X k-blocked: tiles_m*BM rows, ldc columns
-                *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + xoff(1, int64_t(g.tiles_m) * BM, g.ldc, orow, ocol)) =
-                    wv;
+            } else if constexpr (KB) {  // X, A or B k-blocked: tiles_m*BM rows
+                *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + xoff(1, int64_t(g.tiles_m) * BM, 0, orow, ocol)) = wv;
             } else {
                 *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + orow * g.ldc + ocol) = wv;
             }
@@ -726,16 +754,12 @@ hipError_t launch_gemm(int tile, const GemmArgs& g, const MuonBatchDescs& d, int
     dim3 grid(unsigned(ga.tiles_per_matrix) * unsigned(batch));
     const int32_t kid = MODE == MODE_GRAM ? K_NS_GRAM : MODE == MODE_POLY ? K_NS_POLY
                       : MODE == MODE_UPDATE ? K_NS_UPDATE : K_NS_APPLY;
-    const bool kb = (MODE == MODE_GRAM || MODE == MODE_UPDATE) && g.xkb;
+    const bool kb = g.xkb != 0;
     const int32_t variant = 2 * tile + (kb ? 1 : 0);  // tile and the KB template flag
-    if constexpr (MODE == MODE_GRAM || MODE == MODE_UPDATE) {
-        if (kb) {
-            if (tile == 256)
-                return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, true>, grid, dim3(kGemmThreads), s,
-                              ga, d);
-            return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE, true>, grid, dim3(kGemmThreads), s,
-                          ga, d);
-        }
+    if (kb) {
+        if (tile == 256)
+            return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, true>, grid, dim3(kGemmThreads), s, ga, d);
+        return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE, true>, grid, dim3(kGemmThreads), s, ga, d);
     }
     if (tile == 256)
         return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, false>, grid, dim3(kGemmThreads), s, ga, d);
@@ -848,7 +872,8 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
     pa.tiles_j = int(p.np / kPrepTile);
     pa.w_mom = float(1.0 - beta);
     pa.w_nest = float(beta);
-    // X k-blocked whenever a whole matrix's byte offsets fit the 31-bit buffer offsets.
+    // Workspace matrices k-blocked whenever a whole matrix's byte offsets fit the
+    // 31-bit buffer offsets.
     pa.xkb = (p.mp * p.np * 2 < (int64_t(1) << 31)) ? 1 : 0;
     const double B = double(batch), m = double(p.m), n = double(p.n);
     dim3 pgrid(unsigned(p.prep_tiles), unsigned(batch));
@@ -879,7 +904,9 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
         gg.xkb = pa.xkb;
         e = launch_gemm<MODE_GRAM>(p.tile, gg, descs, batch, f_gram, s);
         if (e != hipSuccess) return int(e);
-        e = launch_gemm<MODE_POLY>(p.tile, poly_args(A, Bm, p.mp, p.tile, b, c), descs, batch, f_poly, s);
+        GemmArgs gp = poly_args(A, Bm, p.mp, p.tile, b, c);
+        gp.xkb = pa.xkb;
+        e = launch_gemm<MODE_POLY>(p.tile, gp, descs, batch, f_poly, s);
         if (e != hipSuccess) return int(e);
         GemmArgs gu = update_args(Bm, XT[cur], X, last ? nullptr : XT[cur ^ 1], p.mp, p.np, p.tile, a);
         gu.xkb = pa.xkb;
