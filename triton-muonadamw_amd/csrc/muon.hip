@@ -82,50 +82,79 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
     const uint16_t* gh = reinterpret_cast<const uint16_t*>(d.grad);
     const bool vec = ((C & 3) == 0) && (reinterpret_cast<uintptr_t>(d.grad) & (gb ? 7 : 15)) == 0 &&
                      (reinterpret_cast<uintptr_t>(d.mom) & 15) == 0;
+    // The four passes' gradient and momentum loads are issued before any
+    // store (the stores could alias later loads as far as the compiler knows,
+    // which would otherwise serialise the passes).
+    float u[4][4];
+    if (vec) {
+        float g[4][4], m[4][4];
+        bool ok[4];
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+            const int64_t r = r0 + rr + 16 * pass;
+            ok[pass] = r < R && c < C;
+            if (ok[pass]) {
+                const int64_t off = r * C + c;
+                if (gb) {
+                    const uint2 w = *reinterpret_cast<const uint2*>(gh + off);
+                    g[pass][0] = bf16_to_f32(w.x & 0xffffu);
+                    g[pass][1] = bf16_to_f32(w.x >> 16);
+                    g[pass][2] = bf16_to_f32(w.y & 0xffffu);
+                    g[pass][3] = bf16_to_f32(w.y >> 16);
+                } else {
+                    const float4 g4 = *reinterpret_cast<const float4*>(d.grad + off);
+                    g[pass][0] = g4.x;
+                    g[pass][1] = g4.y;
+                    g[pass][2] = g4.z;
+                    g[pass][3] = g4.w;
+                }
+                const float4 m4 = *reinterpret_cast<const float4*>(d.mom + off);
+                m[pass][0] = m4.x;
+                m[pass][1] = m4.y;
+                m[pass][2] = m4.z;
+                m[pass][3] = m4.w;
+            }
+        }
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) u[pass][e] = 0.f;
+            if (ok[pass]) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    m[pass][e] = lerp_torch(m[pass][e], g[pass][e], a.w_mom);
+                    u[pass][e] = NESTEROV ? lerp_torch(g[pass][e], m[pass][e], a.w_nest) : m[pass][e];
+                }
+                const int64_t off = (r0 + rr + 16 * pass) * C + c;
+                *reinterpret_cast<float4*>(d.mom + off) = make_float4(m[pass][0], m[pass][1], m[pass][2], m[pass][3]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int pass = 0; pass < 4; ++pass) {
+            const int64_t r = r0 + rr + 16 * pass;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) u[pass][e] = 0.f;
+            if (r < R && c < C) {
+                const int64_t off = r * C + c;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (c + e < C) {
+                        const float gv = gb ? bf16_to_f32(gh[off + e]) : d.grad[off + e];
+                        const float mv = lerp_torch(d.mom[off + e], gv, a.w_mom);
+                        d.mom[off + e] = mv;
+                        u[pass][e] = NESTEROV ? lerp_torch(gv, mv, a.w_nest) : mv;
+                    }
+                }
+            }
+        }
+    }
     float ss = 0.f;
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
         const int rl = rr + 16 * pass;
         const int64_t r = r0 + rl;
-        float u[4] = {0.f, 0.f, 0.f, 0.f};
-        if (r < R && c < C) {
-            const int64_t off = r * C + c;
-            if (vec) {
-                float g[4];
-                if (gb) {
-                    const uint2 w = *reinterpret_cast<const uint2*>(gh + off);
-                    g[0] = bf16_to_f32(w.x & 0xffffu);
-                    g[1] = bf16_to_f32(w.x >> 16);
-                    g[2] = bf16_to_f32(w.y & 0xffffu);
-                    g[3] = bf16_to_f32(w.y >> 16);
-                } else {
-                    const float4 g4 = *reinterpret_cast<const float4*>(d.grad + off);
-                    g[0] = g4.x;
-                    g[1] = g4.y;
-                    g[2] = g4.z;
-                    g[3] = g4.w;
-                }
-                float4 m4 = *reinterpret_cast<const float4*>(d.mom + off);
-                float m[4] = {m4.x, m4.y, m4.z, m4.w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    m[e] = lerp_torch(m[e], g[e], a.w_mom);
-                    u[e] = NESTEROV ? lerp_torch(g[e], m[e], a.w_nest) : m[e];
-                }
-                *reinterpret_cast<float4*>(d.mom + off) = make_float4(m[0], m[1], m[2], m[3]);
-            } else {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    if (c + e < C) {
-                        const float g = gb ? bf16_to_f32(gh[off + e]) : d.grad[off + e];
-                        const float m = lerp_torch(d.mom[off + e], g, a.w_mom);
-                        d.mom[off + e] = m;
-                        u[e] = NESTEROV ? lerp_torch(g, m, a.w_nest) : m;
-                    }
-                }
-            }
-        }
-        const uint2 pk = make_uint2(pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3]));
+        const uint2 pk = make_uint2(pack_bf16x2(u[pass][0], u[pass][1]), pack_bf16x2(u[pass][2], u[pass][3]));
         const uint32_t h[4] = {pk.x & 0xffffu, pk.x >> 16, pk.y & 0xffffu, pk.y >> 16};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -185,13 +214,17 @@ __global__ __launch_bounds__(256) void muon_scale_kernel(const PrepArgs a, const
     uint16_t* XT = a.xt + bat * a.np * a.mp;
     const float s = inv[bat];
     const int cg = tid & 15, rr = tid >> 4;
+    uint2 v[4];  // all four loads before the in-place stores
+#pragma unroll
+    for (int pass = 0; pass < 4; ++pass)
+        v[pass] = *reinterpret_cast<const uint2*>(X + xoff(a.xkb, a.mp, a.np, i0 + rr + 16 * pass, j0 + cg * 4));
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
         const int rl = rr + 16 * pass;
         uint2* p = reinterpret_cast<uint2*>(X + xoff(a.xkb, a.mp, a.np, i0 + rl, j0 + cg * 4));
-        const uint2 v = *p;
-        const uint2 w = make_uint2(pack_bf16x2(bf16_to_f32(v.x & 0xffffu) * s, bf16_to_f32(v.x >> 16) * s),
-                                   pack_bf16x2(bf16_to_f32(v.y & 0xffffu) * s, bf16_to_f32(v.y >> 16) * s));
+        const uint2 w =
+            make_uint2(pack_bf16x2(bf16_to_f32(v[pass].x & 0xffffu) * s, bf16_to_f32(v[pass].x >> 16) * s),
+                       pack_bf16x2(bf16_to_f32(v[pass].y & 0xffffu) * s, bf16_to_f32(v[pass].y >> 16) * s));
         *p = w;
         tileT[cg * 4 + 0][rl] = uint16_t(w.x);
         tileT[cg * 4 + 1][rl] = uint16_t(w.x >> 16);
