@@ -370,64 +370,82 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, int(bytes), 0x00020000);
 }
 
-// APPLY on up to 8 consecutive elements of one parameter row: with u the bf16
-// update values in w, param[prow][pcol+e] = param*keep - slr*u (and upd = u)
-// for e < min(cap, left).
-__device__ __forceinline__ void apply_chunk(const MuonMatDesc& d, uint4 w, int64_t prow, int64_t pcol, int64_t cap,
-                                            int64_t left, float keep) {
+// APPLY on up to 8 consecutive elements of one parameter row, in two halves so
+// that a caller can issue the parameter loads of several pieces before any
+// store (to the compiler a store could alias a later load, which would
+// otherwise serialise the pieces behind the HBM latency): with u the bf16
+// update values in w, param[idx + e] = param*keep - slr*u (and upd = u) for
+// e < nv.  apply_begin loads the parameter when the piece is 8 elements on
+// 16-byte boundaries (the common case); the caller then sets w, and
+// apply_end finishes the piece, or does it element by element otherwise.
+struct ApplyPiece {
+    uint4 w;       // bf16 update values
+    uint4 p0, p1;  // fp32 parameter: two float4 bit patterns; bf16 parameter: p0
+    int64_t idx;   // parameter element index of the first value
+    int nv;        // values to apply (0..8)
+    bool fast;     // p0 / p1 hold the loaded parameter
+};
+
+__device__ __forceinline__ void apply_begin(const MuonMatDesc& d, ApplyPiece& a, int64_t prow, int64_t pcol,
+                                            int64_t cap, int64_t left) {
     const int64_t nv = cap < left ? cap : left;
-    if (nv <= 0) return;
-    const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+    a.nv = nv > 0 ? int(nv) : 0;
+    a.idx = prow * d.cols + pcol;
+    const bool bf = (d.flags & MAMW_BF16_PARAM) != 0;
+    const uintptr_t pa = bf ? reinterpret_cast<uintptr_t>(reinterpret_cast<uint16_t*>(d.param) + a.idx)
+                            : reinterpret_cast<uintptr_t>(d.param + a.idx);
+    const uintptr_t ua = d.upd ? reinterpret_cast<uintptr_t>(d.upd + a.idx) : 0;
+    a.fast = a.nv == 8 && ((pa | ua) & 15) == 0;
+    if (a.fast) {
+        const uint4* q = reinterpret_cast<const uint4*>(pa);
+        a.p0 = q[0];
+        if (!bf) a.p1 = q[1];
+    }
+}
+
+__device__ __forceinline__ void apply_end(const MuonMatDesc& d, const ApplyPiece& a, float keep) {
+    if (a.nv == 0) return;
+    const uint32_t ww[4] = {a.w.x, a.w.y, a.w.z, a.w.w};
     float u[8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         u[2 * j] = bf16_to_f32(ww[j] & 0xffffu);
         u[2 * j + 1] = bf16_to_f32(ww[j] >> 16);
     }
-    const int64_t idx = prow * d.cols + pcol;
-    float* up = d.upd ? d.upd + idx : nullptr;
-    if (d.flags & MAMW_BF16_PARAM) {  // bf16 parameter: fp32 arithmetic, rounded back to nearest-even
-        uint16_t* ph = reinterpret_cast<uint16_t*>(d.param) + idx;
-        if (nv == 8 && ((reinterpret_cast<uintptr_t>(ph) | reinterpret_cast<uintptr_t>(up)) & 15) == 0) {
-            const uint4 pw = *reinterpret_cast<const uint4*>(ph);
-            const uint32_t pv[4] = {pw.x, pw.y, pw.z, pw.w};
+    float* up = d.upd ? d.upd + a.idx : nullptr;
+    if (a.fast) {
+        if (d.flags & MAMW_BF16_PARAM) {  // bf16 parameter: fp32 arithmetic, rounded back to nearest-even
+            const uint32_t pv[4] = {a.p0.x, a.p0.y, a.p0.z, a.p0.w};
             uint32_t o[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 o[j] = pack_bf16x2(__builtin_fmaf(-d.slr, u[2 * j], bf16_to_f32(pv[j] & 0xffffu) * keep),
                                    __builtin_fmaf(-d.slr, u[2 * j + 1], bf16_to_f32(pv[j] >> 16) * keep));
-            *reinterpret_cast<uint4*>(ph) = make_uint4(o[0], o[1], o[2], o[3]);
-            if (up) {
-                reinterpret_cast<float4*>(up)[0] = make_float4(u[0], u[1], u[2], u[3]);
-                reinterpret_cast<float4*>(up)[1] = make_float4(u[4], u[5], u[6], u[7]);
-            }
+            *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(d.param) + a.idx) = make_uint4(o[0], o[1], o[2], o[3]);
         } else {
-            for (int e = 0; e < nv; ++e) {
-                ph[e] = uint16_t(f32_to_bf16(__builtin_fmaf(-d.slr, u[e], bf16_to_f32(ph[e]) * keep)));
-                if (up) up[e] = u[e];
-            }
+            const uint32_t pv[8] = {a.p0.x, a.p0.y, a.p0.z, a.p0.w, a.p1.x, a.p1.y, a.p1.z, a.p1.w};
+            float o[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = __builtin_fmaf(-d.slr, u[j], __uint_as_float(pv[j]) * keep);
+            float4* p = reinterpret_cast<float4*>(d.param + a.idx);
+            p[0] = make_float4(o[0], o[1], o[2], o[3]);
+            p[1] = make_float4(o[4], o[5], o[6], o[7]);
         }
-        return;
-    }
-    float* p = d.param + idx;
-    if (nv == 8 && ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(up)) & 15) == 0) {
-        float4 p0 = reinterpret_cast<const float4*>(p)[0], p1 = reinterpret_cast<const float4*>(p)[1];
-        p0.x = __builtin_fmaf(-d.slr, u[0], p0.x * keep);
-        p0.y = __builtin_fmaf(-d.slr, u[1], p0.y * keep);
-        p0.z = __builtin_fmaf(-d.slr, u[2], p0.z * keep);
-        p0.w = __builtin_fmaf(-d.slr, u[3], p0.w * keep);
-        p1.x = __builtin_fmaf(-d.slr, u[4], p1.x * keep);
-        p1.y = __builtin_fmaf(-d.slr, u[5], p1.y * keep);
-        p1.z = __builtin_fmaf(-d.slr, u[6], p1.z * keep);
-        p1.w = __builtin_fmaf(-d.slr, u[7], p1.w * keep);
-        reinterpret_cast<float4*>(p)[0] = p0;
-        reinterpret_cast<float4*>(p)[1] = p1;
         if (up) {
             reinterpret_cast<float4*>(up)[0] = make_float4(u[0], u[1], u[2], u[3]);
             reinterpret_cast<float4*>(up)[1] = make_float4(u[4], u[5], u[6], u[7]);
         }
+        return;
+    }
+    if (d.flags & MAMW_BF16_PARAM) {
+        uint16_t* ph = reinterpret_cast<uint16_t*>(d.param) + a.idx;
+        for (int e = 0; e < a.nv; ++e) {
+            ph[e] = uint16_t(f32_to_bf16(__builtin_fmaf(-d.slr, u[e], bf16_to_f32(ph[e]) * keep)));
+            if (up) up[e] = u[e];
+        }
     } else {
-        for (int e = 0; e < nv; ++e) {
+        float* p = d.param + a.idx;
+        for (int e = 0; e < a.nv; ++e) {
             p[e] = __builtin_fmaf(-d.slr, u[e], p[e] * keep);
             if (up) up[e] = u[e];
         }
@@ -646,29 +664,40 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     }
 
     // Lane holds, for fragment (a,b) and register group q, rows y..y+3 of
-    // column x: one 8-byte TT cell, combined with src in place.
+    // column x: one 8-byte TT cell, combined with src in place.  The 4F
+    // cells of a fragment row are all read before any is written (to the
+    // compiler a write could alias a later read, which would serialise every
+    // cell behind the LDS latency).
+    auto cell = [&](int a, int b, int q) {
+        const int y = wm * WT + a * 32 + q * 8 + (lane >> 5) * 4;
+        const int x = wn * WT + b * 32 + (lane & 31);
+        return reinterpret_cast<uint2*>(TT + tt(x, y));
+    };
 #pragma unroll
     for (int a = 0; a < F; ++a) {
+        uint2 s2[F][4];
+        if constexpr (MODE != MODE_GRAM) {
+#pragma unroll
+            for (int b = 0; b < F; ++b)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) s2[b][q] = *cell(a, b, q);
+        }
 #pragma unroll
         for (int b = 0; b < F; ++b) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                const int y = wm * WT + a * 32 + q * 8 + (lane >> 5) * 4;
-                const int x = wn * WT + b * 32 + (lane & 31);
-                uint2* cell = reinterpret_cast<uint2*>(TT + tt(x, y));
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = acc[a][b][q * 4 + e];
                 if constexpr (MODE != MODE_GRAM) {
-                    const uint2 s2 = *cell;
-                    const float sv[4] = {bf16_to_f32(s2.x & 0xffffu), bf16_to_f32(s2.x >> 16),
-                                         bf16_to_f32(s2.y & 0xffffu), bf16_to_f32(s2.y >> 16)};
+                    const float sv[4] = {bf16_to_f32(s2[b][q].x & 0xffffu), bf16_to_f32(s2[b][q].x >> 16),
+                                         bf16_to_f32(s2[b][q].y & 0xffffu), bf16_to_f32(s2[b][q].y >> 16)};
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         v[e] = MODE == MODE_POLY ? __builtin_fmaf(g.alpha, v[e], g.beta * sv[e])
                                                  : __builtin_fmaf(g.beta, sv[e], v[e]);
                 }
-                *cell = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+                *cell(a, b, q) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
             }
         }
     }
@@ -698,20 +727,39 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         // k-blocked outputs: each wave writes 8 rows x 128 bytes of one panel
         // (one contiguous KB); otherwise 2 rows x 32 chunks.
         constexpr bool PANEL = KB && MODE != MODE_APPLY;
+        constexpr int NT = BN * NCH / kGemmThreads;  // per thread
+        if constexpr (MODE == MODE_APPLY) {
+            // Parameter rows of a tall matrix, in batches of U pieces: all U
+            // parameter loads, then the U updates.  (Keeping the next batch's
+            // loads in flight while finishing one measured no faster: the
+            // parameter traffic of all CUs at once is what bounds this part.)
+            constexpr int U = 8;
+            static_assert(NT % U == 0, "whole batches");
+            for (int it0 = 0; it0 < NT; it0 += U) {
+                ApplyPiece pc[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int k = (it0 + u) * kGemmThreads + tid;
+                    const int x = k / NCH, c = k % NCH;
+                    const int64_t orow = int64_t(tj) * BN + x, ocol = int64_t(ti) * BM + c * 8;
+                    apply_begin(d, pc[u], orow, ocol, orow < g.n ? int64_t(8) : int64_t(0), g.m - ocol);
+                    pc[u].w = *reinterpret_cast<const uint4*>(TT + x * BM + (((c ^ x ^ (x >> 3)) & (NCH - 1)) << 3));
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) apply_end(d, pc[u], g.keep);
+            }
+        } else {
 #pragma unroll 8
-        for (int it = 0; it < BN * NCH / kGemmThreads; ++it) {
-            const int k = it * kGemmThreads + tid;
-            const int x = PANEL ? (k >> 3) % BN : k / NCH;
-            const int c = PANEL ? ((k >> 3) / BN) * 8 + (k & 7) : k % NCH;
-            const uint4 w = *reinterpret_cast<const uint4*>(TT + x * BM + (((c ^ x ^ (x >> 3)) & (NCH - 1)) << 3));
-            const int64_t orow = int64_t(tj) * BN + x, ocol = int64_t(ti) * BM + c * 8;
-            if constexpr (MODE == MODE_APPLY) {
-                apply_chunk(d, w, orow, ocol, orow < g.n ? int64_t(8) : int64_t(0), g.m - ocol, g.keep);
-            } else if constexpr (SYM) {
-                *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + (KB ? xoff(1, rows_t, 0, orow, ocol) : orow * g.ldc + ocol)) = w;
-            } else {
-                *reinterpret_cast<uint4*>(g.ct + bat * g.ct_bs + (KB ? xoff(1, rows_t, 0, orow, ocol) : orow * g.ldct + ocol)) =
-                    w;
+            for (int it = 0; it < NT; ++it) {
+                const int k = it * kGemmThreads + tid;
+                const int x = PANEL ? (k >> 3) % BN : k / NCH;
+                const int c = PANEL ? ((k >> 3) / BN) * 8 + (k & 7) : k % NCH;
+                const uint4 w =
+                    *reinterpret_cast<const uint4*>(TT + x * BM + (((c ^ x ^ (x >> 3)) & (NCH - 1)) << 3));
+                const int64_t orow = int64_t(tj) * BN + x, ocol = int64_t(ti) * BM + c * 8;
+                uint16_t* dst = SYM ? g.c + bat * g.c_bs + (KB ? xoff(1, rows_t, 0, orow, ocol) : orow * g.ldc + ocol)
+                                    : g.ct + bat * g.ct_bs + (KB ? xoff(1, rows_t, 0, orow, ocol) : orow * g.ldct + ocol);
+                *reinterpret_cast<uint4*>(dst) = w;
             }
         }
     }
@@ -727,21 +775,43 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         constexpr int NXQ = BN / 32;                // 32-column pieces of a 16-row band
         constexpr int NIT = (BM / 16) * NXQ / 4;    // per wave
         const int gi = lane & 15, grp = lane >> 4;
-#pragma unroll 4
-        for (int it = 0; it < NIT; ++it) {
+        auto coords = [&](int it, int64_t& orow, int64_t& ocol) {
+            const int t = it * 4 + wave;
+            orow = int64_t(ti) * BM + (t / NXQ) * 16 + gi;
+            ocol = int64_t(tj) * BN + (t % NXQ) * 32 + grp * 8;
+        };
+        auto gather = [&](int it, int64_t& orow, int64_t& ocol) {
             const int t = it * 4 + wave;
             const int yb = (t / NXQ) * 16, xc = (t % NXQ) * 32 + grp * 8;
             const int xr = xc + (gi >> 2), yr = yb + 4 * (gi & 3);
             const uint2 lo = lds_read_tr16(TT + tt(xr, yr)), hi = lds_read_tr16(TT + tt(xr + 4, yr));
-            const uint4 wv = make_uint4(lo.x, lo.y, hi.x, hi.y);
-            const int y = yb + gi;
-            const int64_t orow = int64_t(ti) * BM + y, ocol = int64_t(tj) * BN + xc;
-            if constexpr (MODE == MODE_APPLY) {
-                apply_chunk(d, wv, orow, ocol, orow < g.m ? int64_t(8) : int64_t(0), g.n - ocol, g.keep);
-            } else if constexpr (KB) {  // X, A or B k-blocked: tiles_m*BM rows
-                *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + xoff(1, int64_t(g.tiles_m) * BM, 0, orow, ocol)) = wv;
-            } else {
-                *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + orow * g.ldc + ocol) = wv;
+            coords(it, orow, ocol);
+            return make_uint4(lo.x, lo.y, hi.x, hi.y);
+        };
+        if constexpr (MODE == MODE_APPLY) {
+            // Parameter rows of a wide matrix, in batches of U pieces: all U
+            // parameter loads, then the U updates.
+            constexpr int U = 8;
+            static_assert(NIT % U == 0, "whole batches");
+            for (int it0 = 0; it0 < NIT; it0 += U) {
+                ApplyPiece pc[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    int64_t orow, ocol;
+                    pc[u].w = gather(it0 + u, orow, ocol);
+                    apply_begin(d, pc[u], orow, ocol, orow < g.m ? int64_t(8) : int64_t(0), g.n - ocol);
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) apply_end(d, pc[u], g.keep);
+            }
+        } else {
+#pragma unroll 4
+            for (int it = 0; it < NIT; ++it) {
+                int64_t orow, ocol;
+                const uint4 wv = gather(it, orow, ocol);
+                const int64_t off = KB ? xoff(1, int64_t(g.tiles_m) * BM, 0, orow, ocol)  // X, A or B k-blocked
+                                       : orow * g.ldc + ocol;
+                *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + off) = wv;
             }
         }
     }
