@@ -8,7 +8,7 @@ step (lower is better).  Extras on the same JSON line:
 
 * gpt2   : full step, GPT-2-124M-shaped set (config 4), ms per step
 * adamw  : AdamW-only step on config 2 (256 tensors, 2**26 elements), HBM GB/s
-* ns     : Muon-only step on the config 3 matrices, NS MFMA TFLOP/s and % of peak
+* ns     : Muon-only step on the config 3 matrices, NS TFLOP/s and % of peak over the step's device time
 
 `roofline` describes the dominant kernel of the headline step (the one with
 the largest total device time), from per-dispatch HIP events recorded by the
@@ -145,7 +145,8 @@ def bench_full_step(layout, dev, steps, warmup, seed, label):
     log(f"[{label}] {sum(p.numel() for _, p, _ in named):,} params; warmup {warmup}, timed {steps}")
     ms, wall, recs = time_steps(opt, steps, warmup, profile=True)
     agg = summarize_kernels(recs)
-    log(f"[{label}] {ms:.3f} ms/step (device events), {wall:.3f} ms/step (host wall)")
+    note = " (shape classes concurrent: kernel times below overlap)" if opt.muon._concurrent else ""
+    log(f"[{label}] {ms:.3f} ms/step (device events), {wall:.3f} ms/step (host wall){note}")
     for k, a in sorted(agg.items(), key=lambda kv: -kv[1]["ms"]):
         tf = a["flops"] / (a["ms"] * 1e-3) / 1e12 if a["flops"] else 0.0
         log(f"    {k:42s} {a['launches']:4d} launches {a['ms'] / steps:9.3f} ms/step  {tf:8.1f} TFLOP/s")
@@ -202,17 +203,19 @@ def bench_ns_c3(dev, steps, warmup):
                   ns_steps=5, eps=mc.eps)
     for p in params:
         opt.momentum[p].normal_(0.0, 1e-3, generator=gen)
-    ms, wall, recs = time_steps(opt, steps, warmup, profile=True)
-    gemm = [r for r in recs if r["kernel"].startswith("ns_gemm_kernel")]
-    gemm_ms = sum(r["ms"] for r in gemm) / steps
+    ms, wall, recs = time_steps(opt, steps, warmup, profile=False)
+    # The four shape classes of this small step run concurrently on side
+    # streams, so kernel durations overlap: the rate is taken over the whole
+    # step's device time (prep, norm and scale included), a lower bound on the
+    # GEMMs' own rate.
     flops = sum(ns_flops(s) for s in C3_SHAPES)
-    tf = flops / (gemm_ms * 1e-3) / 1e12
-    log(f"[ns c3] step {ms:.3f} ms, NS GEMMs {gemm_ms:.3f} ms -> {tf:.1f} TFLOP/s "
-        f"({100 * tf / PEAK_BF16_TFLOPS:.1f}% of bf16 peak)")
+    tf = flops / (ms * 1e-3) / 1e12
+    log(f"[ns c3] step {ms:.3f} ms ({'concurrent' if opt._concurrent else 'in order'} shape classes) -> "
+        f"{tf:.1f} TFLOP/s of NS work over the whole step ({100 * tf / PEAK_BF16_TFLOPS:.1f}% of bf16 peak)")
     del opt, params
     torch.cuda.empty_cache()
-    return {"step_ms": round(ms, 4), "ns_gemm_ms": round(gemm_ms, 4), "TFLOP/s": round(tf, 1),
-            "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4), "ns_flops": flops}
+    return {"step_ms": round(ms, 4), "TFLOP/s_over_step": round(tf, 1),
+            "mfma_frac_over_step": round(tf / PEAK_BF16_TFLOPS, 4), "ns_flops": flops}
 
 
 def cpu_baseline(layout, seed: int = 0, budget_s: float = 30.0):

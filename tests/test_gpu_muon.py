@@ -159,6 +159,37 @@ def test_batched_equals_single(gpu):
         assert torch.equal(a.detach(), b.detach())
 
 
+@pytest.mark.parametrize("on_side_stream", [False, True])
+def test_concurrent_classes_equal_in_order(gpu, on_side_stream):
+    """Shape classes on their own streams (small steps) give the same bits as one after another,
+    also when the caller steps on a non-default stream and reads the result there."""
+    shapes = [(256, 512)] * 3 + [(512, 256)] * 2 + [(384, 384)] * 2 + [(128, 640)]
+    ps, gs, ms = muon_inputs(shapes, seed=7)
+    runs = []
+    for limit in (0.0, HipMuon.concurrent_flops_limit):
+        params = []
+        for p, g in zip(ps, gs):
+            q = torch.nn.Parameter(p.to(gpu))
+            q.grad = g.to(gpu)
+            params.append(q)
+        opt = HipMuon(params, lr=1e-3, coeffs=COEFFS)
+        opt.concurrent_flops_limit = limit
+        for q, m in zip(params, ms):
+            opt.momentum[q].copy_(m)
+        stream = torch.cuda.Stream(device=gpu) if on_side_stream else torch.cuda.current_stream(gpu)
+        stream.wait_stream(torch.cuda.current_stream(gpu))
+        with torch.cuda.stream(stream):
+            for _ in range(3):
+                opt.step()
+            assert opt._concurrent == (limit > 0)
+            out = [q.detach().clone() for q in params] + [opt.momentum[q].clone() for q in params]
+        torch.cuda.current_stream(gpu).wait_stream(stream)
+        runs.append(out)
+    torch.cuda.synchronize()
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("shape", [(768, 3072), (1024, 4096), (4096, 4096), (14336, 4096)])
 def test_config3_ns_vs_torch(gpu, shape):
     """Config 3 shapes: blend momentum (beta 0.95, Nesterov), NS in bf16 vs torch's routine on the GPU."""
