@@ -421,7 +421,8 @@ __device__ __forceinline__ void apply_end(const MuonMatDesc& d, const ApplyPiece
             for (int j = 0; j < 4; ++j)
                 o[j] = pack_bf16x2(__builtin_fmaf(-d.slr, u[2 * j], bf16_to_f32(pv[j] & 0xffffu) * keep),
                                    __builtin_fmaf(-d.slr, u[2 * j + 1], bf16_to_f32(pv[j] >> 16) * keep));
-            *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(d.param) + a.idx) = make_uint4(o[0], o[1], o[2], o[3]);
+            uint16_t* ph = reinterpret_cast<uint16_t*>(d.param) + a.idx;
+            *reinterpret_cast<uint4*>(ph) = make_uint4(o[0], o[1], o[2], o[3]);
         } else {
             const uint32_t pv[8] = {a.p0.x, a.p0.y, a.p0.z, a.p0.w, a.p1.x, a.p1.y, a.p1.z, a.p1.w};
             float o[8];
@@ -525,11 +526,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         for (int b = 0; b < F; ++b)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[a][b][e] = 0.f;
-    // One slice: MFMAs on (ca, cb); reads of the next slice into (na, nb) when
-    // `reads`; the DMA of step k0/kBK into buffer lbuf when `loads`.  All flags
-    // are compile-time constants at every call, so the body has no branches.
     // Epilogue coefficient tile (POLY: A; UPDATE/APPLY: X^T), stored
-    // transposed in LDS as TT[x][y] = src[(tj*BN + x) * lds + ti*BM + y] (A is
+    // transposed in LDS as TT[x][y] = src[tj*BN + x][ti*BM + y] (A is
     // symmetric; X^T holds X transposed), in 1-KB DMA blocks: block b fills TT
     // rows b*RPI .. b*RPI+RPI-1.  TT row x holds 16-byte chunks of BM/8 y
     // values, logical chunk c at physical chunk c ^ (x ^ x>>3) (mod BM/8).
@@ -757,8 +755,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
                 const uint4 w =
                     *reinterpret_cast<const uint4*>(TT + x * BM + (((c ^ x ^ (x >> 3)) & (NCH - 1)) << 3));
                 const int64_t orow = int64_t(tj) * BN + x, ocol = int64_t(ti) * BM + c * 8;
-                uint16_t* dst = SYM ? g.c + bat * g.c_bs + (KB ? xoff(1, rows_t, 0, orow, ocol) : orow * g.ldc + ocol)
-                                    : g.ct + bat * g.ct_bs + (KB ? xoff(1, rows_t, 0, orow, ocol) : orow * g.ldct + ocol);
+                // Symmetric products: the mirror block (rows_t = mp); UPDATE: X^T (rows_t = np).
+                const int64_t off = KB ? xoff(1, rows_t, 0, orow, ocol) : orow * (SYM ? g.ldc : g.ldct) + ocol;
+                uint16_t* dst = SYM ? g.c + bat * g.c_bs + off : g.ct + bat * g.ct_bs + off;
                 *reinterpret_cast<uint4*>(dst) = w;
             }
         }
@@ -859,14 +858,14 @@ hipError_t launch_gemm(int tile, const GemmArgs& g, const MuonBatchDescs& d, int
                       : MODE == MODE_UPDATE ? K_NS_UPDATE : K_NS_APPLY;
     const bool kb = g.xkb != 0;
     const int32_t variant = 2 * tile + (kb ? 1 : 0);  // tile and the KB template flag
+    const dim3 block(kGemmThreads);
     if (kb) {
         if (tile == 256)
-            return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, true>, grid, dim3(kGemmThreads), s, ga, d);
-        return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE, true>, grid, dim3(kGemmThreads), s, ga, d);
+            return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, true>, grid, block, s, ga, d);
+        return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE, true>, grid, block, s, ga, d);
     }
-    if (tile == 256)
-        return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, false>, grid, dim3(kGemmThreads), s, ga, d);
-    return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE, false>, grid, dim3(kGemmThreads), s, ga, d);
+    if (tile == 256) return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, false>, grid, block, s, ga, d);
+    return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE, false>, grid, block, s, ga, d);
 }
 
 GemmArgs gram_args(const uint16_t* X, uint16_t* A, int64_t mp, int64_t kp, int tile) {
