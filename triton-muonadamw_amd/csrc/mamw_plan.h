@@ -60,7 +60,7 @@ int adamw_table_pack_ex(const mamw_adamw_tensor_ex* tensors, int n_tensors,
 //   B   [batch][mp][mp]   b A + c A A
 //   part[batch][prep_tiles] fp32 partial sums of squares (one per prep tile)
 //   inv [batch]           fp32 1 / max(bf16(||X||_F), eps)
-constexpr int kPrepTile = 64;  // prep works on 64 x 64 tiles of X
+constexpr int kPrepTile = 64;  // a prep tile holds 64 x 64 elements of X (32 x 128 when wide)
 constexpr size_t kWsAlign = 256;
 
 struct MuonMatDesc {

@@ -38,7 +38,10 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
 }
 
 // ---------------------------------------------------------------------------
-// Prep: one 64 x 64 tile of X (in X coordinates) per block.
+// Prep: one tile of 4096 elements of X per block: 32 x 128 (X coordinates) for
+// a wide matrix, so each row is read in 512-byte runs (64 x 64 measured 6%
+// slower), and 64 x 64 for a tall one, which goes through LDS to be
+// transposed.
 
 struct PrepArgs {
     uint16_t* x;    // [batch][mp][np], k-blocked when xkb (see xoff)
@@ -46,7 +49,7 @@ struct PrepArgs {
     float* part;    // [batch][prep_tiles]
     int64_t mp, np;
     int64_t prep_tiles;
-    int tiles_j;    // np / 64
+    int tiles_j;    // np / 64 (the scale kernel's 64 x 64 tiles)
     float w_mom;    // 1 - beta   (lerp weight of the momentum update)
     float w_nest;   // beta       (lerp weight of the Nesterov blend)
     int xkb;        // workspace matrices are k-blocked
@@ -69,14 +72,17 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
     const int bat = blockIdx.y;
     const MuonMatDesc& d = descs.d[bat];
     const int64_t q = blockIdx.x;
-    const int64_t i0 = (q / a.tiles_j) * 64, j0 = (q % a.tiles_j) * 64;
     const bool tall = d.tall != 0;
+    const int64_t tw = a.np / 128;  // wide tiles per X row band
+    const int64_t i0 = tall ? (q / a.tiles_j) * 64 : (q / tw) * 32, j0 = tall ? (q % a.tiles_j) * 64 : (q % tw) * 128;
     // Tile origin in parameter coordinates (rows r, cols c of the parameter).
     const int64_t r0 = tall ? j0 : i0, c0 = tall ? i0 : j0;
     const int64_t R = d.rows, C = d.cols;
     uint16_t* X = a.x + bat * a.mp * a.np;
 
-    const int cg = tid & 15, rr = tid >> 4;
+    // Thread tid covers 4 consecutive columns (cg) of rows rr + RP * pass.
+    const int cg = tall ? tid & 15 : tid & 31, rr = tall ? tid >> 4 : tid >> 5;
+    const int RP = tall ? 16 : 8;
     const int64_t c = c0 + cg * 4;
     const bool gb = (d.flags & MAMW_BF16_GRAD) != 0;  // gradient holds bf16
     const uint16_t* gh = reinterpret_cast<const uint16_t*>(d.grad);
@@ -91,7 +97,7 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
         bool ok[4];
 #pragma unroll
         for (int pass = 0; pass < 4; ++pass) {
-            const int64_t r = r0 + rr + 16 * pass;
+            const int64_t r = r0 + rr + RP * pass;
             ok[pass] = r < R && c < C;
             if (ok[pass]) {
                 const int64_t off = r * C + c;
@@ -125,14 +131,14 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
                     m[pass][e] = lerp_torch(m[pass][e], g[pass][e], a.w_mom);
                     u[pass][e] = NESTEROV ? lerp_torch(g[pass][e], m[pass][e], a.w_nest) : m[pass][e];
                 }
-                const int64_t off = (r0 + rr + 16 * pass) * C + c;
+                const int64_t off = (r0 + rr + RP * pass) * C + c;
                 *reinterpret_cast<float4*>(d.mom + off) = make_float4(m[pass][0], m[pass][1], m[pass][2], m[pass][3]);
             }
         }
     } else {
 #pragma unroll
         for (int pass = 0; pass < 4; ++pass) {
-            const int64_t r = r0 + rr + 16 * pass;
+            const int64_t r = r0 + rr + RP * pass;
 #pragma unroll
             for (int e = 0; e < 4; ++e) u[pass][e] = 0.f;
             if (r < R && c < C) {
@@ -152,7 +158,7 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
     float ss = 0.f;
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
-        const int rl = rr + 16 * pass;
+        const int rl = rr + RP * pass;
         const int64_t r = r0 + rl;
         const uint2 pk = make_uint2(pack_bf16x2(u[pass][0], u[pass][1]), pack_bf16x2(u[pass][2], u[pass][3]));
         const uint32_t h[4] = {pk.x & 0xffffu, pk.x >> 16, pk.y & 0xffffu, pk.y >> 16};
