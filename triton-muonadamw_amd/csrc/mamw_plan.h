@@ -58,9 +58,9 @@ int adamw_table_pack_ex(const mamw_adamw_tensor_ex* tensors, int n_tensors,
 //   XT1 [batch][np][mp]   (only when ns_steps >= 2)
 //   A   [batch][mp][mp]   Gram X X^T
 //   B   [batch][mp][mp]   b A + c A A
-//   part[batch][prep_tiles] fp32 partial sums of squares (one per prep tile)
+//   part[batch][prep_tiles] fp32 partial sums of squares (one per prep unit)
 //   inv [batch]           fp32 1 / max(bf16(||X||_F), eps)
-constexpr int kPrepTile = 64;  // a prep tile holds 64 x 64 elements of X (32 x 128 when wide)
+constexpr int kPrepTile = 64;  // a prep unit holds kPrepTile^2 = 32 x 128 parameter elements
 constexpr size_t kWsAlign = 256;
 
 struct MuonMatDesc {
@@ -83,7 +83,7 @@ struct MuonPlan {
     int batch;
     int tile;  // GEMM tile edge (128 or 256); mp, np are multiples of it
     int64_t m, n, mp, np;
-    int64_t prep_tiles;  // (mp/64) * (np/64)
+    int64_t prep_tiles;  // prep units, (mp/64) * (np/64); the prep kernel takes two per block
     size_t off_x, off_xt0, off_xt1, off_a, off_b, off_part, off_inv;
     size_t bytes;
 };

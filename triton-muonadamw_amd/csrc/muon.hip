@@ -38,10 +38,10 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
 }
 
 // ---------------------------------------------------------------------------
-// Prep: one tile of 4096 elements of X per block: 32 x 128 (X coordinates) for
-// a wide matrix, so each row is read in 512-byte runs (64 x 64 measured 6%
-// slower), and 64 x 64 for a tall one, which goes through LDS to be
-// transposed.
+// Prep: one tile of 64 x 128 parameter elements per block, two prep units
+// of 32 rows (parameter rows read in 512-byte runs; 64 x 64 tiles measured 6%
+// slower).  A wide matrix writes it as a 64 x 128 tile of X; a tall one
+// transposes it through LDS into 128 full 128-byte rows of X.
 
 struct PrepArgs {
     uint16_t* x;    // [batch][mp][np], k-blocked when xkb (see xoff)
@@ -66,38 +66,39 @@ __device__ __forceinline__ int64_t xoff(int xkb, int64_t rows, int64_t cols, int
 
 template <bool NESTEROV>
 __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs descs, const PrepArgs a) {
-    __shared__ uint16_t tileT[64][64 + 2];
-    __shared__ float red[4];
+    __shared__ uint16_t tileT[128][64 + 2];
+    __shared__ float red[2][4];
     const int tid = threadIdx.x;
     const int bat = blockIdx.y;
     const MuonMatDesc& d = descs.d[bat];
     const int64_t q = blockIdx.x;
     const bool tall = d.tall != 0;
-    const int64_t tw = a.np / 128;  // wide tiles per X row band
-    const int64_t i0 = tall ? (q / a.tiles_j) * 64 : (q / tw) * 32, j0 = tall ? (q % a.tiles_j) * 64 : (q % tw) * 128;
-    // Tile origin in parameter coordinates (rows r, cols c of the parameter).
-    const int64_t r0 = tall ? j0 : i0, c0 = tall ? i0 : j0;
+    // Consecutive blocks take consecutive 128-column pieces of the same 64
+    // parameter rows.  X coordinates: wide (i0, j0) = (r0, c0); tall (c0, r0).
+    const int64_t bands = tall ? a.mp / 128 : a.np / 128;  // 128-column pieces per parameter row band
+    const int64_t r0 = (q / bands) * 64, c0 = (q % bands) * 128;  // tile origin in the parameter
     const int64_t R = d.rows, C = d.cols;
     uint16_t* X = a.x + bat * a.mp * a.np;
 
-    // Thread tid covers 4 consecutive columns (cg) of rows rr + RP * pass.
-    const int cg = tall ? tid & 15 : tid & 31, rr = tall ? tid >> 4 : tid >> 5;
-    const int RP = tall ? 16 : 8;
+    // Thread tid covers 4 consecutive columns (cg) of rows rr + 8 * pass;
+    // passes 0-3 are the first prep unit (rows 0-31), 4-7 the second.
+    constexpr int NP = 8;
+    const int cg = tid & 31, rr = tid >> 5;
     const int64_t c = c0 + cg * 4;
     const bool gb = (d.flags & MAMW_BF16_GRAD) != 0;  // gradient holds bf16
     const uint16_t* gh = reinterpret_cast<const uint16_t*>(d.grad);
     const bool vec = ((C & 3) == 0) && (reinterpret_cast<uintptr_t>(d.grad) & (gb ? 7 : 15)) == 0 &&
                      (reinterpret_cast<uintptr_t>(d.mom) & 15) == 0;
-    // The four passes' gradient and momentum loads are issued before any
-    // store (the stores could alias later loads as far as the compiler knows,
-    // which would otherwise serialise the passes).
-    float u[4][4];
+    // All passes' gradient and momentum loads are issued before any store
+    // (the stores could alias later loads as far as the compiler knows, which
+    // would otherwise serialise the passes).
+    float u[NP][4];
     if (vec) {
-        float g[4][4], m[4][4];
-        bool ok[4];
+        float g[NP][4], m[NP][4];
+        bool ok[NP];
 #pragma unroll
-        for (int pass = 0; pass < 4; ++pass) {
-            const int64_t r = r0 + rr + RP * pass;
+        for (int pass = 0; pass < NP; ++pass) {
+            const int64_t r = r0 + rr + 8 * pass;
             ok[pass] = r < R && c < C;
             if (ok[pass]) {
                 const int64_t off = r * C + c;
@@ -122,7 +123,7 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
             }
         }
 #pragma unroll
-        for (int pass = 0; pass < 4; ++pass) {
+        for (int pass = 0; pass < NP; ++pass) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) u[pass][e] = 0.f;
             if (ok[pass]) {
@@ -131,14 +132,14 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
                     m[pass][e] = lerp_torch(m[pass][e], g[pass][e], a.w_mom);
                     u[pass][e] = NESTEROV ? lerp_torch(g[pass][e], m[pass][e], a.w_nest) : m[pass][e];
                 }
-                const int64_t off = (r0 + rr + RP * pass) * C + c;
+                const int64_t off = (r0 + rr + 8 * pass) * C + c;
                 *reinterpret_cast<float4*>(d.mom + off) = make_float4(m[pass][0], m[pass][1], m[pass][2], m[pass][3]);
             }
         }
     } else {
 #pragma unroll
-        for (int pass = 0; pass < 4; ++pass) {
-            const int64_t r = r0 + rr + RP * pass;
+        for (int pass = 0; pass < NP; ++pass) {
+            const int64_t r = r0 + rr + 8 * pass;
 #pragma unroll
             for (int e = 0; e < 4; ++e) u[pass][e] = 0.f;
             if (r < R && c < C) {
@@ -155,17 +156,17 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
             }
         }
     }
-    float ss = 0.f;
+    float ss[2] = {0.f, 0.f};
 #pragma unroll
-    for (int pass = 0; pass < 4; ++pass) {
-        const int rl = rr + RP * pass;
+    for (int pass = 0; pass < NP; ++pass) {
+        const int rl = rr + 8 * pass;
         const int64_t r = r0 + rl;
         const uint2 pk = make_uint2(pack_bf16x2(u[pass][0], u[pass][1]), pack_bf16x2(u[pass][2], u[pass][3]));
         const uint32_t h[4] = {pk.x & 0xffffu, pk.x >> 16, pk.y & 0xffffu, pk.y >> 16};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const float xb = bf16_to_f32(h[e]);
-            ss += xb * xb;
+            ss[pass >> 2] += xb * xb;
         }
         if (!tall) {  // X = bf16(u): parameter rows are X rows
             *reinterpret_cast<uint2*>(X + xoff(a.xkb, a.mp, a.np, r, c)) = pk;
@@ -174,19 +175,25 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
             for (int e = 0; e < 4; ++e) tileT[cg * 4 + e][rl] = uint16_t(h[e]);
         }
     }
-    ss = wave_sum(ss);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    if (tid == 0) a.part[bat * a.prep_tiles + q] = (red[0] + red[1]) + (red[2] + red[3]);
-    if (tall) {  // X = bf16(u)^T: row (c0 + tr) of X, 16 consecutive elements per thread
-        const int tr = tid >> 2, seg = (tid & 3) * 16;
-        uint32_t w[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
+    for (int hf = 0; hf < 2; ++hf) {
+        const float sw = wave_sum(ss[hf]);
+        if ((tid & 63) == 0) red[hf][tid >> 6] = sw;
+    }
+    __syncthreads();
+    if (tid < 2) {  // unit (32-row band 2 * (q / bands) + tid, piece q % bands)
+        const int64_t unit = (2 * (q / bands) + tid) * bands + q % bands;
+        a.part[bat * a.prep_tiles + unit] = (red[tid][0] + red[tid][1]) + (red[tid][2] + red[tid][3]);
+    }
+    if (tall) {  // X = bf16(u)^T: row (c0 + tr) of X, 32 consecutive elements per thread
+        const int tr = tid >> 1, seg = (tid & 1) * 32;
+        uint32_t w[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
             w[k] = uint32_t(tileT[tr][seg + 2 * k]) | (uint32_t(tileT[tr][seg + 2 * k + 1]) << 16);
         uint4* dst = reinterpret_cast<uint4*>(X + xoff(a.xkb, a.mp, a.np, c0 + tr, r0 + seg));
-        dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-        dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) dst[k] = make_uint4(w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]);
     }
 }
 
@@ -984,7 +991,7 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
     // 31-bit buffer offsets.
     pa.xkb = (p.mp * p.np * 2 < (int64_t(1) << 31)) ? 1 : 0;
     const double B = double(batch), m = double(p.m), n = double(p.n);
-    dim3 pgrid(unsigned(p.prep_tiles), unsigned(batch));
+    dim3 pgrid(unsigned(p.prep_tiles / 2), unsigned(batch));  // two prep units per block
     // prep: read grad, momentum; write momentum, X (4 + 4 + 4 + 2 bytes per element)
     const double prep_bytes = 14.0 * B * m * n;
     hipError_t e = nesterov ? launch(K_MUON_PREP, 1, 0.0, prep_bytes, muon_prep_kernel<true>, pgrid, dim3(256), s,
@@ -995,8 +1002,9 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
     e = launch(K_MUON_NORM, 0, 0.0, 4.0 * B * double(p.prep_tiles), muon_norm_kernel, dim3(unsigned(batch)),
                dim3(256), s, static_cast<const float*>(part), p.prep_tiles, eps, inv);
     if (e != hipSuccess) return int(e);
-    // scale: read X; write X, XT (2 + 2 + 2 bytes per padded element)
-    e = launch(K_MUON_SCALE, 0, 0.0, 6.0 * B * double(p.mp) * double(p.np), muon_scale_kernel, pgrid, dim3(256), s,
+    // scale: read X; write X, XT (2 + 2 + 2 bytes per padded element), one 64 x 64 tile per block
+    const dim3 sgrid(unsigned(p.prep_tiles), unsigned(batch));
+    e = launch(K_MUON_SCALE, 0, 0.0, 6.0 * B * double(p.mp) * double(p.np), muon_scale_kernel, sgrid, dim3(256), s,
                pa, static_cast<const float*>(inv));
     if (e != hipSuccess) return int(e);
 
