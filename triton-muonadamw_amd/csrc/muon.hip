@@ -49,7 +49,7 @@ struct PrepArgs {
     float* part;    // [batch][prep_tiles]
     int64_t mp, np;
     int64_t prep_tiles;
-    int tiles_j;    // np / 64 (the scale kernel's 64 x 64 tiles)
+    int tiles_j;    // np / 64 (the scale kernel's tiles per 128-row band of X)
     float w_mom;    // 1 - beta   (lerp weight of the momentum update)
     float w_nest;   // beta       (lerp weight of the Nesterov blend)
     int xkb;        // workspace matrices are k-blocked
@@ -217,41 +217,41 @@ __global__ __launch_bounds__(256) void muon_norm_kernel(const float* __restrict_
     }
 }
 
-// X <- bf16(X * inv[b]) in place and XT = X^T, one 64 x 64 tile per block.
+// X <- bf16(X * inv[b]) in place and XT = X^T, one 128 x 64 tile of X per
+// block (two prep units), 16-byte accesses throughout: in the k-blocked layout
+// the X tile is one contiguous 16 KB block and its transpose two 8 KB ones.
 __global__ __launch_bounds__(256) void muon_scale_kernel(const PrepArgs a, const float* __restrict__ inv) {
-    __shared__ uint16_t tileT[64][64 + 2];
+    __shared__ uint16_t tileT[64][128 + 8];  // rows of 272 bytes: 16-byte aligned, spread over the banks
     const int tid = threadIdx.x, bat = blockIdx.y;
     const int64_t q = blockIdx.x;
-    const int64_t i0 = (q / a.tiles_j) * 64, j0 = (q % a.tiles_j) * 64;
+    const int64_t i0 = (q / a.tiles_j) * 128, j0 = (q % a.tiles_j) * 64;
     uint16_t* X = a.x + bat * a.mp * a.np;
     uint16_t* XT = a.xt + bat * a.np * a.mp;
     const float s = inv[bat];
-    const int cg = tid & 15, rr = tid >> 4;
-    uint2 v[4];  // all four loads before the in-place stores
+    const int cg = tid & 7, rr = tid >> 3;  // columns cg*8 .. cg*8+7 of rows rr + 32 * pass
+    uint4 v[4];  // all four loads before the in-place stores
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass)
-        v[pass] = *reinterpret_cast<const uint2*>(X + xoff(a.xkb, a.mp, a.np, i0 + rr + 16 * pass, j0 + cg * 4));
+        v[pass] = *reinterpret_cast<const uint4*>(X + xoff(a.xkb, a.mp, a.np, i0 + rr + 32 * pass, j0 + cg * 8));
 #pragma unroll
     for (int pass = 0; pass < 4; ++pass) {
-        const int rl = rr + 16 * pass;
-        uint2* p = reinterpret_cast<uint2*>(X + xoff(a.xkb, a.mp, a.np, i0 + rl, j0 + cg * 4));
-        const uint2 w =
-            make_uint2(pack_bf16x2(bf16_to_f32(v[pass].x & 0xffffu) * s, bf16_to_f32(v[pass].x >> 16) * s),
-                       pack_bf16x2(bf16_to_f32(v[pass].y & 0xffffu) * s, bf16_to_f32(v[pass].y >> 16) * s));
-        *p = w;
-        tileT[cg * 4 + 0][rl] = uint16_t(w.x);
-        tileT[cg * 4 + 1][rl] = uint16_t(w.x >> 16);
-        tileT[cg * 4 + 2][rl] = uint16_t(w.y);
-        tileT[cg * 4 + 3][rl] = uint16_t(w.y >> 16);
+        const int rl = rr + 32 * pass;
+        const uint4 w = scale_bf16x8(v[pass], s);
+        *reinterpret_cast<uint4*>(X + xoff(a.xkb, a.mp, a.np, i0 + rl, j0 + cg * 8)) = w;
+        const uint32_t wv[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            tileT[cg * 8 + 2 * k][rl] = uint16_t(wv[k]);
+            tileT[cg * 8 + 2 * k + 1][rl] = uint16_t(wv[k] >> 16);
+        }
     }
     __syncthreads();
-    const int tr = tid >> 2, seg = (tid & 3) * 16;
-    uint32_t w[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) w[k] = uint32_t(tileT[tr][seg + 2 * k]) | (uint32_t(tileT[tr][seg + 2 * k + 1]) << 16);
+    // XT row (j0 + tr), elements i0 + seg .. i0 + seg + 31: 64 contiguous bytes per thread.
+    const int tr = tid >> 2, seg = (tid & 3) * 32;
+    const uint4* src = reinterpret_cast<const uint4*>(&tileT[tr][seg]);
     uint4* dst = reinterpret_cast<uint4*>(XT + xoff(a.xkb, a.np, a.mp, j0 + tr, i0 + seg));
-    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) dst[k] = src[k];
 }
 
 // ns_steps == 0: the update is the normalised X itself.
@@ -1002,8 +1002,8 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
     e = launch(K_MUON_NORM, 0, 0.0, 4.0 * B * double(p.prep_tiles), muon_norm_kernel, dim3(unsigned(batch)),
                dim3(256), s, static_cast<const float*>(part), p.prep_tiles, eps, inv);
     if (e != hipSuccess) return int(e);
-    // scale: read X; write X, XT (2 + 2 + 2 bytes per padded element), one 64 x 64 tile per block
-    const dim3 sgrid(unsigned(p.prep_tiles), unsigned(batch));
+    // scale: read X; write X, XT (2 + 2 + 2 bytes per padded element), two prep units per block
+    const dim3 sgrid(unsigned(p.prep_tiles / 2), unsigned(batch));
     e = launch(K_MUON_SCALE, 0, 0.0, 6.0 * B * double(p.mp) * double(p.np), muon_scale_kernel, sgrid, dim3(256), s,
                pa, static_cast<const float*>(inv));
     if (e != hipSuccess) return int(e);
