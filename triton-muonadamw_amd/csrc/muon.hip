@@ -679,10 +679,19 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     // cells of a fragment row are all read before any is written (to the
     // compiler a write could alias a later read, which would serialise every
     // cell behind the LDS latency).
-    auto cell = [&](int a, int b, int q) {
-        const int y = wm * WT + a * 32 + q * 8 + (lane >> 5) * 4;
+    // With x = wn*WT + 32b + (lane & 31) and y = wm*WT + 32a + 8q + 4(lane >> 5),
+    // y >> 3 = yc is wave-uniform and below NCH, so tt(x, y) in bytes is
+    // xb2[b] + ((yc << 4) ^ xs4[b]): one xor-add per cell.
+    int xb2[F], xs4[F];
+#pragma unroll
+    for (int b = 0; b < F; ++b) {
         const int x = wn * WT + b * 32 + (lane & 31);
-        return reinterpret_cast<uint2*>(TT + tt(x, y));
+        xb2[b] = (x * BM + (lane >> 5) * 4) * 2;
+        xs4[b] = ((x ^ (x >> 3)) & (NCH - 1)) << 4;
+    }
+    auto cell = [&](int a, int b, int q) {
+        const int yc = (wm * WT + a * 32 + q * 8) >> 3;
+        return reinterpret_cast<uint2*>(reinterpret_cast<char*>(TT) + (((yc << 4) ^ xs4[b]) + xb2[b]));
     };
 #pragma unroll
     for (int a = 0; a < F; ++a) {
