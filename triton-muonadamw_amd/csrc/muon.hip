@@ -693,8 +693,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         const int yc = (wm * WT + a * 32 + q * 8) >> 3;
         return reinterpret_cast<uint2*>(reinterpret_cast<char*>(TT) + (((yc << 4) ^ xs4[b]) + xb2[b]));
     };
-#pragma unroll
-    for (int a = 0; a < F; ++a) {
+    auto combine_row = [&](int a) {
         uint2 s2[F][4];
         if constexpr (MODE != MODE_GRAM) {
 #pragma unroll
@@ -720,7 +719,102 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
                 *cell(a, b, q) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
             }
         }
+    };
+
+    const MuonMatDesc& d = descs.d[bat];
+    const bool tall = MODE == MODE_APPLY && d.tall;
+    // Transposed orientation, from TT rows: row (tj*BN + x) of the output holds
+    // TT row x.  Symmetric products: the mirror block (the tile itself on the
+    // diagonal); UPDATE: X^T; APPLY: the parameter of a tall matrix.
+    // k-blocked outputs: each wave writes 8 rows x 128 bytes of one panel (one
+    // contiguous KB) per piece, and piece `it` covers tile rows y in
+    // [64 (it / 8), +64) when BM = 256; otherwise 2 rows x 32 chunks.
+    const bool has_tr = SYM || (MODE == MODE_UPDATE && g.ct) || tall;
+    constexpr bool PANEL = KB && MODE != MODE_APPLY;
+    constexpr int NT = BN * NCH / kGemmThreads;  // transposed pieces per thread
+    auto store_tr = [&](int it) {
+        const int k = it * kGemmThreads + tid;
+        const int x = PANEL ? (k >> 3) % BN : k / NCH;
+        const int c = PANEL ? ((k >> 3) / BN) * 8 + (k & 7) : k % NCH;
+        const uint4 w = *reinterpret_cast<const uint4*>(TT + x * BM + (((c ^ x ^ (x >> 3)) & (NCH - 1)) << 3));
+        const int64_t orow = int64_t(tj) * BN + x, ocol = int64_t(ti) * BM + c * 8;
+        // Symmetric products: the mirror block (rows_t = mp); UPDATE: X^T (rows_t = np).
+        const int64_t off = KB ? xoff(1, rows_t, 0, orow, ocol) : orow * (SYM ? g.ldc : g.ldct) + ocol;
+        uint16_t* dst = SYM ? g.c + bat * g.c_bs + off : g.ct + bat * g.ct_bs + off;
+        *reinterpret_cast<uint4*>(dst) = w;
+    };
+    // Direct orientation, gathered from TT columns: row (ti*BM + y) of the
+    // output holds TT[x][y] over x.  Symmetric products: the tile's own block
+    // (off the diagonal); UPDATE: X; APPLY: the parameter of a wide matrix.
+    // Two transpose reads give a lane 8 consecutive columns of one row: in a
+    // 16-lane group, lane j names TT[xc + j/4][yb + 4(j%4) ..], so lane i
+    // receives C[yb + i][xc .. xc+3] (and xc+4 .. xc+7 from the second read).
+    // A group covers 16 rows x 8 columns, the 4 groups of a wave adjacent
+    // 8-column pieces of the same rows (2-way LDS bank conflicts at most);
+    // piece `it` covers rows y in [16 (it / 2), +16) when BM = 256.
+    const bool has_dir = (SYM && !diag) || MODE == MODE_UPDATE || (MODE == MODE_APPLY && !tall);
+    constexpr int NXQ = BN / 32;                // 32-column pieces of a 16-row band
+    constexpr int NIT = (BM / 16) * NXQ / 4;    // direct pieces per wave
+    const int gi = lane & 15, grp = lane >> 4;
+    auto coords = [&](int it, int64_t& orow, int64_t& ocol) {
+        const int t = it * 4 + wave;
+        orow = int64_t(ti) * BM + (t / NXQ) * 16 + gi;
+        ocol = int64_t(tj) * BN + (t % NXQ) * 32 + grp * 8;
+    };
+    auto gather = [&](int it, int64_t& orow, int64_t& ocol) {
+        const int t = it * 4 + wave;
+        const int yb = (t / NXQ) * 16, xc = (t % NXQ) * 32 + grp * 8;
+        const int xr = xc + (gi >> 2), yr = yb + 4 * (gi & 3);
+        const uint2 lo = lds_read_tr16(TT + tt(xr, yr)), hi = lds_read_tr16(TT + tt(xr + 4, yr));
+        coords(it, orow, ocol);
+        return make_uint4(lo.x, lo.y, hi.x, hi.y);
+    };
+    auto store_dir = [&](int it) {
+        int64_t orow, ocol;
+        const uint4 wv = gather(it, orow, ocol);
+        const int64_t off = KB ? xoff(1, int64_t(g.tiles_m) * BM, 0, orow, ocol)  // X, A or B k-blocked
+                               : orow * g.ldc + ocol;
+        *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + off) = wv;
+    };
+
+    // 256-wide k-blocked tiles off the diagonal: combine fragment rows 0-1
+    // (tile rows y in [0, 64) and [128, 192), both wave rows), store those
+    // bands, then combine rows 2-3 while the first stores drain.  The two
+    // halves touch disjoint TT cells.
+    constexpr bool SPLIT = BM == 256 && PANEL;
+    bool split_done = false;
+    if constexpr (SPLIT) {
+        static_assert(F == 4 && NT == 32 && NIT == 32, "band layout of the 256 tile");
+        if (!diag) {
+            auto store_bands = [&](int ph) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int it0 = (2 * h + ph) * 8;
+                    if (has_tr) {
+#pragma unroll 8
+                        for (int it = it0; it < it0 + 8; ++it) store_tr(it);
+                    }
+                    if (has_dir) {
+#pragma unroll 4
+                        for (int it = it0; it < it0 + 8; ++it) store_dir(it);
+                    }
+                }
+            };
+            combine_row(0);
+            combine_row(1);
+            __syncthreads();
+            store_bands(0);
+            combine_row(2);
+            combine_row(3);
+            __syncthreads();
+            store_bands(1);
+            split_done = true;
+        }
     }
+    if (split_done) return;
+
+#pragma unroll
+    for (int a = 0; a < F; ++a) combine_row(a);
     __syncthreads();
     if (diag) {
         // Diagonal tile of a symmetric product: the upper triangle (y <= x) is
@@ -738,16 +832,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         __syncthreads();
     }
 
-    // Transposed orientation, from TT rows: row (tj*BN + x) of the output holds
-    // TT row x.  Symmetric products: the mirror block (the tile itself on the
-    // diagonal); UPDATE: X^T; APPLY: the parameter of a tall matrix.
-    const MuonMatDesc& d = descs.d[bat];
-    const bool tall = MODE == MODE_APPLY && d.tall;
-    if (SYM || (MODE == MODE_UPDATE && g.ct) || tall) {
-        // k-blocked outputs: each wave writes 8 rows x 128 bytes of one panel
-        // (one contiguous KB); otherwise 2 rows x 32 chunks.
-        constexpr bool PANEL = KB && MODE != MODE_APPLY;
-        constexpr int NT = BN * NCH / kGemmThreads;  // per thread
+
+    if (has_tr) {
         if constexpr (MODE == MODE_APPLY) {
             // Parameter rows of a tall matrix, in batches of U pieces: all U
             // parameter loads, then the U updates.  (Keeping the next batch's
@@ -770,45 +856,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
             }
         } else {
 #pragma unroll 8
-            for (int it = 0; it < NT; ++it) {
-                const int k = it * kGemmThreads + tid;
-                const int x = PANEL ? (k >> 3) % BN : k / NCH;
-                const int c = PANEL ? ((k >> 3) / BN) * 8 + (k & 7) : k % NCH;
-                const uint4 w =
-                    *reinterpret_cast<const uint4*>(TT + x * BM + (((c ^ x ^ (x >> 3)) & (NCH - 1)) << 3));
-                const int64_t orow = int64_t(tj) * BN + x, ocol = int64_t(ti) * BM + c * 8;
-                // Symmetric products: the mirror block (rows_t = mp); UPDATE: X^T (rows_t = np).
-                const int64_t off = KB ? xoff(1, rows_t, 0, orow, ocol) : orow * (SYM ? g.ldc : g.ldct) + ocol;
-                uint16_t* dst = SYM ? g.c + bat * g.c_bs + off : g.ct + bat * g.ct_bs + off;
-                *reinterpret_cast<uint4*>(dst) = w;
-            }
+            for (int it = 0; it < NT; ++it) store_tr(it);
         }
     }
-    // Direct orientation, gathered from TT columns: row (ti*BM + y) of the
-    // output holds TT[x][y] over x.  Symmetric products: the tile's own block
-    // (off the diagonal); UPDATE: X; APPLY: the parameter of a wide matrix.
-    // Two transpose reads give a lane 8 consecutive columns of one row: in a
-    // 16-lane group, lane j names TT[xc + j/4][yb + 4(j%4) ..], so lane i
-    // receives C[yb + i][xc .. xc+3] (and xc+4 .. xc+7 from the second read).
-    // A group covers 16 rows x 8 columns, the 4 groups of a wave adjacent
-    // 8-column pieces of the same rows (2-way LDS bank conflicts at most).
-    if ((SYM && !diag) || MODE == MODE_UPDATE || (MODE == MODE_APPLY && !tall)) {
-        constexpr int NXQ = BN / 32;                // 32-column pieces of a 16-row band
-        constexpr int NIT = (BM / 16) * NXQ / 4;    // per wave
-        const int gi = lane & 15, grp = lane >> 4;
-        auto coords = [&](int it, int64_t& orow, int64_t& ocol) {
-            const int t = it * 4 + wave;
-            orow = int64_t(ti) * BM + (t / NXQ) * 16 + gi;
-            ocol = int64_t(tj) * BN + (t % NXQ) * 32 + grp * 8;
-        };
-        auto gather = [&](int it, int64_t& orow, int64_t& ocol) {
-            const int t = it * 4 + wave;
-            const int yb = (t / NXQ) * 16, xc = (t % NXQ) * 32 + grp * 8;
-            const int xr = xc + (gi >> 2), yr = yb + 4 * (gi & 3);
-            const uint2 lo = lds_read_tr16(TT + tt(xr, yr)), hi = lds_read_tr16(TT + tt(xr + 4, yr));
-            coords(it, orow, ocol);
-            return make_uint4(lo.x, lo.y, hi.x, hi.y);
-        };
+    if (has_dir) {
         if constexpr (MODE == MODE_APPLY) {
             // Parameter rows of a wide matrix, in batches of U pieces: all U
             // parameter loads, then the U updates.
@@ -827,13 +878,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
             }
         } else {
 #pragma unroll 4
-            for (int it = 0; it < NIT; ++it) {
-                int64_t orow, ocol;
-                const uint4 wv = gather(it, orow, ocol);
-                const int64_t off = KB ? xoff(1, int64_t(g.tiles_m) * BM, 0, orow, ocol)  // X, A or B k-blocked
-                                       : orow * g.ldc + ocol;
-                *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + off) = wv;
-            }
+            for (int it = 0; it < NIT; ++it) store_dir(it);
         }
     }
 }
