@@ -3,7 +3,8 @@
 // Launch sequence for one batch of equal-shaped matrices (mamw_muon_step):
 //   1. muon_prep_kernel   momentum lerp, Nesterov blend, bf16 cast (tall
 //                         matrices transposed through LDS); writes X (m x n,
-//                         zero-padded) and one fp32 sum of squares per 64x64 tile.
+//                         zero-padded) and one fp32 sum of squares per prep
+//                         unit of 32 x 128 parameter elements.
 //   2. muon_norm_kernel   fixed-order reduction of those partials ->
 //                         inv[b] = 1 / max(bf16(||X||_F), eps).
 //   3. muon_scale_kernel  X <- bf16(X * inv[b]) in place (torch's X.div_(norm)
