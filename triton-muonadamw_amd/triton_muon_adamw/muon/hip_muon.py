@@ -7,10 +7,11 @@ launchers ``solve_ns_kernel_{1,2,3}`` (:95-117, :191-212, :281-310),
 ``HipMuon.step()`` groups the matrices that have a gradient by
 ``(min(R,C), max(R,C))`` and runs each group as batched launches of
 ``mamw_muon_step`` (at most 32 matrices and a bounded workspace per call):
-prep (momentum, Nesterov, bf16, transpose, sum of squares), norm, then per
-Newton-Schulz iteration a Gram, a polynomial and an update GEMM, the last of
-which writes the parameters.  The reference runs about 30 launches per
-matrix; here a group of up to 32 matrices costs ``2 + 3*ns_steps`` launches.
+prep (momentum, Nesterov, bf16, transpose, sum of squares), norm, scale
+(``X / ||X||`` in bf16 and its transpose), then per Newton-Schulz iteration a
+Gram, a polynomial and an update GEMM, the last of which writes the
+parameters.  The reference runs about 30 launches per matrix; here a group of
+up to 32 matrices costs ``3 + 3*ns_steps`` launches.
 Small steps (``HipMuon.concurrent_flops_limit``) run the shape groups
 concurrently on side streams forked from and joined back into the caller's
 current stream; the results are the same bits as in order.
