@@ -20,6 +20,7 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
 }
 
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 // Two fp32 -> packed bf16x2 (low half = lo), round to nearest even: one

@@ -92,7 +92,9 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
                      (reinterpret_cast<uintptr_t>(d.mom) & 15) == 0;
     // All passes' gradient and momentum loads are issued before any store
     // (the stores could alias later loads as far as the compiler knows, which
-    // would otherwise serialise the passes).
+    // would otherwise serialise the passes).  Gradient and momentum are
+    // streamed non-temporally: nothing reads them again within the step
+    // (4.5-10% faster than cached accesses on the Llama-8B classes).
     float u[NP][4];
     if (vec) {
         float g[NP][4], m[NP][4];
@@ -110,13 +112,13 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
                     g[pass][2] = bf16_to_f32(w.y & 0xffffu);
                     g[pass][3] = bf16_to_f32(w.y >> 16);
                 } else {
-                    const float4 g4 = *reinterpret_cast<const float4*>(d.grad + off);
+                    const f32x4_t g4 = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(d.grad + off));
                     g[pass][0] = g4.x;
                     g[pass][1] = g4.y;
                     g[pass][2] = g4.z;
                     g[pass][3] = g4.w;
                 }
-                const float4 m4 = *reinterpret_cast<const float4*>(d.mom + off);
+                const f32x4_t m4 = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(d.mom + off));
                 m[pass][0] = m4.x;
                 m[pass][1] = m4.y;
                 m[pass][2] = m4.z;
@@ -134,7 +136,8 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
                     u[pass][e] = NESTEROV ? lerp_torch(g[pass][e], m[pass][e], a.w_nest) : m[pass][e];
                 }
                 const int64_t off = (r0 + rr + 8 * pass) * C + c;
-                *reinterpret_cast<float4*>(d.mom + off) = make_float4(m[pass][0], m[pass][1], m[pass][2], m[pass][3]);
+                __builtin_nontemporal_store(f32x4_t{m[pass][0], m[pass][1], m[pass][2], m[pass][3]},
+                                            reinterpret_cast<f32x4_t*>(d.mom + off));
             }
         }
     } else {
