@@ -106,9 +106,21 @@ def _run_muon(shapes, gpu, seed=1, lr=2e-2, **kw):
 SMALL_SHAPES = [(128, 256), (256, 128), (100, 37), (37, 100), (512, 512), (640, 1280), (1, 5), (300, 1)]
 
 
+# Ragged shapes over several prep tiles (64 x 128 parameter elements) and
+# scale tiles (128 x 64 of X) in both orientations, tall and wide in one class.
+RAGGED_SHAPES = [(300, 1000), (1000, 300), (1000, 300), (200, 520), (520, 200)]
+
+
 @pytest.mark.parametrize("nesterov,ns_steps", [(True, 5), (False, 5), (True, 1), (True, 0), (True, 2)])
 def test_muon_step_vs_oracle(gpu, nesterov, ns_steps):
-    shapes = SMALL_SHAPES
+    _check_vs_oracle(gpu, SMALL_SHAPES, nesterov, ns_steps)
+
+
+def test_ragged_multi_tile_vs_oracle(gpu):
+    _check_vs_oracle(gpu, RAGGED_SHAPES, True, 5)
+
+
+def _check_vs_oracle(gpu, shapes, nesterov, ns_steps):
     ps, gs, ms, params, opt = _run_muon(shapes, gpu, nesterov=nesterov, ns_steps=ns_steps)
     outs = []
     for p in params:  # update outputs through muon_step's `out` on a copy of each matrix
