@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MAMW_ABI_VERSION 2
+#define MAMW_ABI_VERSION 3
 
 /* ---- status codes -------------------------------------------------------- */
 #define MAMW_OK             0
@@ -125,6 +125,24 @@ int mamw_adamw_mt_step(const void* device_table, int n_tensors,
                        float beta1, float beta2, float weight_decay, float eps,
                        mamw_stream_t stream);
 
+/* mamw_adamw_mt_step for a gradient-scaler step, with the scaler's tensors
+ * left on the device (no host synchronisation): the fused AdamW path of
+ * torch/optim/adam.py:865-899 driven by torch/amp/grad_scaler.py:403-448
+ * (the reference has no mixed-precision path).
+ *   step:       device fp32 step counter, already incremented for this step;
+ *               the bias corrections are 1 - beta^step, formed on the device
+ *               in double from the double betas and rounded to fp32, as the
+ *               host forms them for mamw_adamw_mt_step.  Required.
+ *   grad_scale: device fp32; every gradient is divided by it.  NULL: none.
+ *   found_inf:  device fp32; non-zero skips the update (parameters and
+ *               moments untouched).  NULL: never skipped.
+ * The caller decrements *step by *found_inf afterwards, as torch does.      */
+int mamw_adamw_mt_step_amp(const void* device_table, int n_tensors,
+                           int64_t n_blocks, float lr, double beta1,
+                           double beta2, float weight_decay, float eps,
+                           const float* step, const float* grad_scale,
+                           const float* found_inf, mamw_stream_t stream);
+
 /* ==== Muon ================================================================= *
  * One Muon update of up to MAMW_MUON_MAX_BATCH matrices that share
  * {min(rows,cols), max(rows,cols)} (wide and tall may be mixed), following
@@ -167,6 +185,18 @@ int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr,
                    double weight_decay, double beta, int nesterov, float a,
                    float b, float c, int ns_steps, float eps, void* workspace,
                    size_t workspace_bytes, mamw_stream_t stream);
+
+/* mamw_muon_step for a gradient-scaler step (torch/amp/grad_scaler.py:403-448;
+ * the reference has no mixed-precision path): gradients are divided by the
+ * device fp32 *grad_scale (NULL: not scaled); a non-zero device fp32
+ * *found_inf (NULL: never) leaves the momentum, the parameters and the update
+ * buffers untouched, with no host synchronisation.                         */
+int mamw_muon_step_amp(const mamw_muon_matrix* mats, int batch, double lr,
+                       double weight_decay, double beta, int nesterov, float a,
+                       float b, float c, int ns_steps, float eps,
+                       void* workspace, size_t workspace_bytes,
+                       const float* grad_scale, const float* found_inf,
+                       mamw_stream_t stream);
 
 /* ==== Newton-Schulz building blocks (batched, bf16, fp32 accumulate) ======== *
  * Operate on `batch` contiguous zero-padded row-major matrices.  m and n must

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_strerror():
     lib = _lib.load()
-    assert lib.mamw_abi_version() == 2
+    assert lib.mamw_abi_version() == 3
     for code in (OK, NULL, COUNT, NUMEL, SHAPE, ALIGN, WS, HYPER, TABLE, ALIAS):
         msg = lib.mamw_strerror(code).decode()
         assert msg and msg != "unknown status"

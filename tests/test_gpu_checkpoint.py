@@ -145,11 +145,18 @@ def test_step_closure_returns_loss(gpu):
     assert not torch.equal(before, w.detach())  # only w has a gradient; it moved
 
 
+def _state(opt):
+    return ([opt.adamw.m[p] for p in opt.adamw.model_params] + [opt.adamw.v[p] for p in opt.adamw.model_params]
+            + [opt.muon.momentum[p] for p in opt.muon.model_params])
+
+
 def test_grad_scaler_unscales_and_skips_inf_steps(gpu):
-    """torch.amp.GradScaler drives MuonAdamW like any torch optimizer: gradients
-    are unscaled in place (power-of-two scale: exact) before step(); a step with
-    a non-finite gradient is skipped entirely (parameters, state and the AdamW
-    step counter untouched), as torch.optim does."""
+    """torch.amp.GradScaler drives MuonAdamW through its device-side path
+    (grad_scale / found_inf handed to step()): gradients are divided by the
+    scale in the kernels (power-of-two scale: exact); a step with a non-finite
+    gradient is skipped entirely on the device (parameters, moments, momentum
+    and the AdamW step counter untouched), as torch's fused AdamW does; the
+    next step's bias corrections come from the device counter."""
     a, b = _params(gpu), _params(gpu)
     opt_a = MuonAdamW(_split(a), muon_config=MC, adam_config=AC, parameter_split="explicit")
     opt_b = MuonAdamW(_split(b), muon_config=MC, adam_config=AC, parameter_split="explicit")
@@ -164,6 +171,7 @@ def test_grad_scaler_unscales_and_skips_inf_steps(gpu):
     scaler.update()
     opt_b.step()
     torch.cuda.synchronize()
+    assert opt_a.adamw._dev_steps, "the scaler did not take the device-side path"
     for (n, p, _), (_, q, _) in zip(a, b):
         assert torch.equal(p.detach(), q.detach()), n
     before = [p.detach().clone() for _, p, _ in a]
@@ -171,8 +179,53 @@ def test_grad_scaler_unscales_and_skips_inf_steps(gpu):
     g[0][0] = float("inf")
     for (_, p, _), gi in zip(a, g):
         p.grad = gi * scaler.get_scale()
+    state_before = [t.clone() for t in _state(opt_a)]
     scaler.step(opt_a)
     scaler.update()
     torch.cuda.synchronize()
     assert all(torch.equal(p.detach(), q) for (_, p, _), q in zip(a, before))
+    assert all(torch.equal(t, u) for t, u in zip(_state(opt_a), state_before))
     assert opt_a.adamw.step_num == 1 and scaler.get_scale() == 512.0
+    # a finite step after the skipped one: step 2 on both sides
+    g = _grads(a, gpu, gen)
+    for (_, p, _), gi in zip(a, g):
+        p.grad = gi * 512.0
+    _set(b, g)
+    scaler.step(opt_a)
+    scaler.update()
+    opt_b.step()
+    torch.cuda.synchronize()
+    for (n, p, _), (_, q, _) in zip(a, b):
+        assert torch.equal(p.detach(), q.detach()), n
+    assert all(torch.equal(t, u) for t, u in zip(_state(opt_a), _state(opt_b)))
+    assert opt_a.adamw.step_num == 2 and opt_b.adamw.step_num == 2
+
+
+def test_grad_scaler_after_explicit_unscale(gpu):
+    """scaler.unscale_(opt) before scaler.step(opt) (e.g. to clip gradients):
+    the scaler then hands over found_inf only; the result equals a plain step
+    on the unscaled gradients, and a non-finite step is still skipped."""
+    a, b = _params(gpu), _params(gpu)
+    opt_a = MuonAdamW(_split(a), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    opt_b = MuonAdamW(_split(b), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    scaler = torch.amp.GradScaler("cuda", init_scale=256.0, growth_interval=1000)
+    scaler.scale(torch.ones((), device=gpu))  # initialise the scale on the device
+    gen = torch.Generator(device=gpu).manual_seed(6)
+    for it in range(3):
+        g = _grads(a, gpu, gen)
+        if it == 1:
+            g[-1][0] = float("nan")
+        scale = scaler.get_scale()
+        for (_, p, _), gi in zip(a, g):
+            p.grad = gi * scale
+        scaler.unscale_(opt_a)
+        scaler.step(opt_a)
+        scaler.update()
+        if it != 1:
+            _set(b, g)
+            opt_b.step()
+    torch.cuda.synchronize()
+    for (n, p, _), (_, q, _) in zip(a, b):
+        assert torch.equal(p.detach(), q.detach()), n
+    assert all(torch.equal(t, u) for t, u in zip(_state(opt_a), _state(opt_b)))
+    assert opt_a.adamw.step_num == 2

@@ -20,6 +20,16 @@ namespace {
 struct AdamWConsts {
     float lr, bias1, bias2, beta1, beta2, eps;
     float omb1, omb2, decay;  // 1-beta1, 1-beta2, 1-lr*weight_decay (fp32, as the reference)
+    // Gradient-scaler step (all NULL otherwise): gradients are divided by
+    // *grad_scale; a non-zero *found_inf skips the update; the bias
+    // corrections come from the device step counter *step, in double from the
+    // double betas, as the host forms them from its own counter.
+    const float* grad_scale;
+    const float* found_inf;
+    const float* step;
+    double beta1d, beta2d;
+    float gs;     // *grad_scale, read by the kernel
+    int scaled;   // grad_scale != NULL
 };
 
 __host__ AdamWConsts make_consts(const AdamWScalars& s) {
@@ -33,7 +43,30 @@ __host__ AdamWConsts make_consts(const AdamWScalars& s) {
     c.omb1 = 1.0f - s.beta1;
     c.omb2 = 1.0f - s.beta2;
     c.decay = 1.0f - s.lr * s.weight_decay;
+    c.grad_scale = c.found_inf = c.step = nullptr;
+    c.beta1d = c.beta2d = 0.0;
+    c.gs = 1.0f;
+    c.scaled = 0;
     return c;
+}
+
+// Per-block set-up of a gradient-scaler step: false when the step is skipped.
+__device__ __forceinline__ bool adamw_prepare(AdamWConsts& c) {
+    if (c.found_inf && *c.found_inf != 0.0f) return false;
+    if (c.step) {
+        const double st = double(*c.step);
+        c.bias1 = float(1.0 - pow(c.beta1d, st));
+        c.bias2 = float(1.0 - pow(c.beta2d, st));
+    }
+    if (c.grad_scale) {
+        c.gs = *c.grad_scale;
+        c.scaled = 1;
+    }
+    return true;
+}
+
+__device__ __forceinline__ float4 unscale4(float4 g, const AdamWConsts& c) {
+    return c.scaled ? make_float4(g.x / c.gs, g.y / c.gs, g.z / c.gs, g.w / c.gs) : g;
 }
 
 __device__ __forceinline__ void adamw_elem(float& p, float g, float& m, float& v,
@@ -126,7 +159,7 @@ __device__ __forceinline__ void adamw_chunk(const AdamWRec& r, int64_t start, in
         for (int u = 0; u < kAdamWUnroll; ++u) {
             const int i = u * kAdamWThreads + tid;
             p[u] = ld4<PB>(r.p, q0 + i);
-            g[u] = ld4<GB>(r.g, q0 + i);
+            g[u] = unscale4(ld4<GB>(r.g, q0 + i), c);
             m[u] = nt_load(M4 + i);
             v[u] = nt_load(V4 + i);
         }
@@ -145,7 +178,7 @@ __device__ __forceinline__ void adamw_chunk(const AdamWRec& r, int64_t start, in
         const int nv = len >> 2;
         for (int i = tid; i < nv; i += kAdamWThreads) {
             float4 p = ld4<PB>(r.p, q0 + i), m = nt_load(M4 + i), v = nt_load(V4 + i);
-            adamw_vec(p, ld4<GB>(r.g, q0 + i), m, v, c);
+            adamw_vec(p, unscale4(ld4<GB>(r.g, q0 + i), c), m, v, c);
             st4<PB>(r.p, q0 + i, p);
             nt_store(M4 + i, m);
             nt_store(V4 + i, v);
@@ -154,7 +187,8 @@ __device__ __forceinline__ void adamw_chunk(const AdamWRec& r, int64_t start, in
     }
     for (int e = scalar_from + tid; e < len; e += kAdamWThreads) {
         float p = ld1<PB>(r.p, start + e), m = M[e], v = V[e];
-        adamw_elem(p, ld1<GB>(r.g, start + e), m, v, c);
+        const float ge = ld1<GB>(r.g, start + e);
+        adamw_elem(p, c.scaled ? ge / c.gs : ge, m, v, c);
         st1<PB>(r.p, start + e, p);
         M[e] = m;
         V[e] = v;
@@ -174,6 +208,7 @@ __device__ __forceinline__ void adamw_chunk_any(const AdamWRec& r, int64_t start
 
 __global__ __launch_bounds__(kAdamWThreads) void adamw_mt_kernel(const AdamWRec* __restrict__ recs,
                                                                   int n, AdamWConsts c) {
+    if (!adamw_prepare(c)) return;
     const int64_t b = blockIdx.x;
     // Largest t with recs[t].block_begin <= b (block_begin is non-decreasing):
     // binary search with scalar loads down to a range of at most 64 records,
@@ -201,6 +236,7 @@ __global__ __launch_bounds__(kAdamWThreads) void adamw_mt_kernel(const AdamWRec*
 }
 
 __global__ __launch_bounds__(kAdamWThreads) void adamw_one_kernel(AdamWRec r, AdamWConsts c) {
+    if (!adamw_prepare(c)) return;
     const int64_t start = int64_t(blockIdx.x) * kAdamWChunk;
     const int64_t rem = r.numel - start;
     adamw_chunk_any(r, start, rem < kAdamWChunk ? int(rem) : int(kAdamWChunk), c);
@@ -240,18 +276,39 @@ extern "C" int mamw_adamw_table_pack_ex(const mamw_adamw_tensor_ex* tensors, int
     return adamw_table_pack_ex(tensors, n_tensors, host_table, table_bytes, n_blocks);
 }
 
-extern "C" int mamw_adamw_mt_step(const void* device_table, int n_tensors, int64_t n_blocks,
-                                  float lr, float bias1, float bias2, float beta1, float beta2,
-                                  float weight_decay, float eps, mamw_stream_t stream) {
+namespace {
+int adamw_mt_launch(const void* device_table, int n_tensors, int64_t n_blocks, const AdamWConsts& c,
+                    mamw_stream_t stream) {
     if (n_tensors < 0 || n_tensors > kMaxTensors) return MAMW_ERR_COUNT;
     if (n_blocks < 0 || n_blocks > int64_t(0x7fffffff)) return MAMW_ERR_NUMEL;
     if (n_blocks == 0) return MAMW_OK;
     if (n_tensors == 0) return MAMW_ERR_COUNT;
     if (!device_table) return MAMW_ERR_NULL;
     if (reinterpret_cast<uintptr_t>(device_table) % 16) return MAMW_ERR_ALIGN;
-    AdamWScalars s{lr, bias1, bias2, beta1, beta2, weight_decay, eps};
     // Algorithmic bytes (28 per element) are not known here: the table is in device memory.
     return int(launch(K_ADAMW_MT, 0, 0.0, 0.0, adamw_mt_kernel, dim3(unsigned(n_blocks)), dim3(kAdamWThreads),
-                      static_cast<hipStream_t>(stream), static_cast<const AdamWRec*>(device_table), n_tensors,
-                      make_consts(s)));
+                      static_cast<hipStream_t>(stream), static_cast<const AdamWRec*>(device_table), n_tensors, c));
+}
+}  // namespace
+
+extern "C" int mamw_adamw_mt_step(const void* device_table, int n_tensors, int64_t n_blocks,
+                                  float lr, float bias1, float bias2, float beta1, float beta2,
+                                  float weight_decay, float eps, mamw_stream_t stream) {
+    AdamWScalars s{lr, bias1, bias2, beta1, beta2, weight_decay, eps};
+    return adamw_mt_launch(device_table, n_tensors, n_blocks, make_consts(s), stream);
+}
+
+extern "C" int mamw_adamw_mt_step_amp(const void* device_table, int n_tensors, int64_t n_blocks,
+                                      float lr, double beta1, double beta2, float weight_decay, float eps,
+                                      const float* step, const float* grad_scale, const float* found_inf,
+                                      mamw_stream_t stream) {
+    if (!step) return MAMW_ERR_NULL;
+    AdamWScalars s{lr, 1.0f, 1.0f, float(beta1), float(beta2), weight_decay, eps};
+    AdamWConsts c = make_consts(s);
+    c.step = step;
+    c.grad_scale = grad_scale;
+    c.found_inf = found_inf;
+    c.beta1d = beta1;
+    c.beta2d = beta2;
+    return adamw_mt_launch(device_table, n_tensors, n_blocks, c, stream);
 }

@@ -54,6 +54,11 @@ struct PrepArgs {
     float w_mom;    // 1 - beta   (lerp weight of the momentum update)
     float w_nest;   // beta       (lerp weight of the Nesterov blend)
     int xkb;        // workspace matrices are k-blocked
+    // Gradient-scaler step (NULL otherwise): gradients are divided by
+    // *grad_scale; a non-zero *found_inf leaves the momentum (and, in the
+    // apply kernels, the parameters) untouched.
+    const float* grad_scale;
+    const float* found_inf;
 };
 
 // Offset of element [r][c] of a rows x cols workspace matrix (X: mp x np,
@@ -90,6 +95,9 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
     const uint16_t* gh = reinterpret_cast<const uint16_t*>(d.grad);
     const bool vec = ((C & 3) == 0) && (reinterpret_cast<uintptr_t>(d.grad) & (gb ? 7 : 15)) == 0 &&
                      (reinterpret_cast<uintptr_t>(d.mom) & 15) == 0;
+    const bool scaled = a.grad_scale != nullptr;
+    const float gsc = scaled ? *a.grad_scale : 1.0f;
+    const bool keep_mom = !(a.found_inf && *a.found_inf != 0.0f);
     // All passes' gradient and momentum loads are issued before any store
     // (the stores could alias later loads as far as the compiler knows, which
     // would otherwise serialise the passes).  Gradient and momentum are
@@ -118,6 +126,10 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
                     g[pass][2] = g4.z;
                     g[pass][3] = g4.w;
                 }
+                if (scaled) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) g[pass][e] /= gsc;
+                }
                 const f32x4_t m4 = __builtin_nontemporal_load(reinterpret_cast<const f32x4_t*>(d.mom + off));
                 m[pass][0] = m4.x;
                 m[pass][1] = m4.y;
@@ -136,8 +148,9 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
                     u[pass][e] = NESTEROV ? lerp_torch(g[pass][e], m[pass][e], a.w_nest) : m[pass][e];
                 }
                 const int64_t off = (r0 + rr + 8 * pass) * C + c;
-                __builtin_nontemporal_store(f32x4_t{m[pass][0], m[pass][1], m[pass][2], m[pass][3]},
-                                            reinterpret_cast<f32x4_t*>(d.mom + off));
+                if (keep_mom)
+                    __builtin_nontemporal_store(f32x4_t{m[pass][0], m[pass][1], m[pass][2], m[pass][3]},
+                                                reinterpret_cast<f32x4_t*>(d.mom + off));
             }
         }
     } else {
@@ -151,9 +164,10 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     if (c + e < C) {
-                        const float gv = gb ? bf16_to_f32(gh[off + e]) : d.grad[off + e];
+                        const float g0 = gb ? bf16_to_f32(gh[off + e]) : d.grad[off + e];
+                        const float gv = scaled ? g0 / gsc : g0;
                         const float mv = lerp_torch(d.mom[off + e], gv, a.w_mom);
-                        d.mom[off + e] = mv;
+                        if (keep_mom) d.mom[off + e] = mv;
                         u[pass][e] = NESTEROV ? lerp_torch(gv, mv, a.w_nest) : mv;
                     }
                 }
@@ -260,6 +274,7 @@ __global__ __launch_bounds__(256) void muon_scale_kernel(const PrepArgs a, const
 
 // ns_steps == 0: the update is the normalised X itself.
 __global__ __launch_bounds__(256) void muon_apply0_kernel(const MuonBatchDescs descs, const PrepArgs a, float keep) {
+    if (a.found_inf && *a.found_inf != 0.0f) return;  // skipped gradient-scaler step
     const int bat = blockIdx.y;
     const MuonMatDesc& d = descs.d[bat];
     const uint16_t* X = a.x + bat * a.mp * a.np;
@@ -319,6 +334,7 @@ struct GemmArgs {
     float keep;           // APPLY: 1 - lr * weight_decay
     int64_t m, n;         // APPLY: valid extent of X
     int xkb;              // operands, coefficient and outputs k-blocked (xoff)
+    const float* found_inf;  // APPLY: a non-zero *found_inf (skipped gradient-scaler step) writes nothing
 };
 
 // Launch block -> (matrix, tile row, tile col).
@@ -487,6 +503,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
+    if constexpr (MODE == MODE_APPLY) {
+        if (g.found_inf && *g.found_inf != 0.0f) return;  // uniform per launch: the whole block leaves
+    }
     int bat, ti, tj;
     decode_tile<SYM>(g, bat, ti, tj);
     // Operand rows of the tile: row-major (row stride ld), or k-blocked (KB:
@@ -1015,10 +1034,11 @@ extern "C" int mamw_muon_workspace_bytes(int batch, int64_t rows, int64_t cols, 
     return MAMW_OK;
 }
 
-extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr, double weight_decay,
-                              double beta, int nesterov, float a, float b, float c, int ns_steps,
-                              float eps, void* workspace, size_t workspace_bytes,
-                              mamw_stream_t stream) {
+namespace {
+int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double weight_decay, double beta,
+                   int nesterov, float a, float b, float c, int ns_steps, float eps, void* workspace,
+                   size_t workspace_bytes, const float* grad_scale, const float* found_inf,
+                   mamw_stream_t stream) {
     MuonPlan p;
     MuonBatchDescs descs;
     int st = muon_validate(mats, batch, ns_steps, workspace, workspace_bytes, &p, &descs);
@@ -1035,7 +1055,7 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
     // Scalars as torch forms them: lerp weights and 1 - lr*wd from double.
     const float keep = float(1.0 - lr * weight_decay);
 
-    PrepArgs pa;
+    PrepArgs pa{};
     pa.x = X;
     pa.xt = XT[0];
     pa.part = part;
@@ -1048,6 +1068,8 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
     // Workspace matrices k-blocked whenever a whole matrix's byte offsets fit the
     // 31-bit buffer offsets.
     pa.xkb = (p.mp * p.np * 2 < (int64_t(1) << 31)) ? 1 : 0;
+    pa.grad_scale = grad_scale;
+    pa.found_inf = found_inf;
     const double B = double(batch), m = double(p.m), n = double(p.n);
     dim3 pgrid(unsigned(p.prep_tiles / 2), unsigned(batch));  // two prep units per block
     // prep: read grad, momentum; write momentum, X (4 + 4 + 4 + 2 bytes per element)
@@ -1085,6 +1107,7 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
         GemmArgs gu = update_args(Bm, XT[cur], X, last ? nullptr : XT[cur ^ 1], p.mp, p.np, p.tile, a);
         gu.xkb = pa.xkb;
         if (last) {
+            gu.found_inf = found_inf;
             gu.keep = keep;
             gu.m = p.m;
             gu.n = p.n;
@@ -1096,6 +1119,23 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
         cur ^= 1;
     }
     return MAMW_OK;
+}
+}  // namespace
+
+extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr, double weight_decay,
+                              double beta, int nesterov, float a, float b, float c, int ns_steps,
+                              float eps, void* workspace, size_t workspace_bytes,
+                              mamw_stream_t stream) {
+    return muon_step_impl(mats, batch, lr, weight_decay, beta, nesterov, a, b, c, ns_steps, eps, workspace,
+                          workspace_bytes, nullptr, nullptr, stream);
+}
+
+extern "C" int mamw_muon_step_amp(const mamw_muon_matrix* mats, int batch, double lr, double weight_decay,
+                                  double beta, int nesterov, float a, float b, float c, int ns_steps,
+                                  float eps, void* workspace, size_t workspace_bytes, const float* grad_scale,
+                                  const float* found_inf, mamw_stream_t stream) {
+    return muon_step_impl(mats, batch, lr, weight_decay, beta, nesterov, a, b, c, ns_steps, eps, workspace,
+                          workspace_bytes, grad_scale, found_inf, stream);
 }
 
 namespace {

@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libmuonadamw_amd.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 MUON_MAX_BATCH = 32
 BF16_PARAM = 0x1  # MAMW_BF16_PARAM
 BF16_GRAD = 0x2   # MAMW_BF16_GRAD
@@ -93,11 +93,21 @@ _PROTOTYPES = {
         [c_void_p, c_int, c_int64, c_float, c_float, c_float, c_float, c_float, c_float, c_float,
          c_void_p],
     ),
+    "mamw_adamw_mt_step_amp": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_float, c_double, c_double, c_float, c_float, c_void_p, c_void_p, c_void_p,
+         c_void_p],
+    ),
     "mamw_muon_workspace_bytes": (c_int, [c_int, c_int64, c_int64, c_int, POINTER(c_size_t)]),
     "mamw_muon_step": (
         c_int,
         [POINTER(MuonMatrix), c_int, c_double, c_double, c_double, c_int, c_float, c_float, c_float,
          c_int, c_float, c_void_p, c_size_t, c_void_p],
+    ),
+    "mamw_muon_step_amp": (
+        c_int,
+        [POINTER(MuonMatrix), c_int, c_double, c_double, c_double, c_int, c_float, c_float, c_float,
+         c_int, c_float, c_void_p, c_size_t, c_void_p, c_void_p, c_void_p],
     ),
     "mamw_ns_gram": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_int64, c_void_p]),
     "mamw_ns_poly": (c_int, [c_void_p, c_void_p, c_int, c_int64, c_float, c_float, c_void_p]),

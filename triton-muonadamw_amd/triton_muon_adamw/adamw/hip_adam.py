@@ -99,7 +99,7 @@ class HipAdamW:
         self.lr = lr
         self.weight_decay = weight_decay
         self.eps = eps
-        self.step_num = 0
+        self.step_num = 0  # also creates the (empty) device-side counters, see step_num
         self.m = {}
         self.v = {}
         for param in self.model_params:
@@ -122,6 +122,27 @@ class HipAdamW:
             by_dev.setdefault(p.device, []).append((p, g, m, v))
         self._plans = [_DevicePlan(dev, ents) for dev, ents in by_dev.items()]
 
+    @property
+    def step_num(self) -> int:
+        """The global step counter (triton_adam.py:137).  After a gradient-scaler
+        step (``_step_amp``) it lives on the device, one fp32 counter per device
+        as torch's fused AdamW keeps it; reading it then synchronises."""
+        if self._dev_steps:
+            return int(next(iter(self._dev_steps.values())).item())
+        return self._step_host
+
+    @step_num.setter
+    def step_num(self, value: int) -> None:
+        self._step_host = int(value)
+        self._dev_steps: dict[torch.device, torch.Tensor] = {}
+
+    def _refresh_plans(self, active: list[nn.Parameter]) -> None:
+        key = tuple((id(p), p.data_ptr(), p.grad.data_ptr(), p.dtype, p.grad.dtype) for p in active)
+        if key != self._plan_key:
+            self._plan_key = None
+            self._build_plans(active)
+            self._plan_key = key
+
     @torch.no_grad()
     def step(self):
         """Performs one iteration of the AdamW optimizer step."""
@@ -129,14 +150,10 @@ class HipAdamW:
         active = [p for p in self.model_params if p.grad is not None]
         if not active:
             return
-        key = tuple((id(p), p.data_ptr(), p.grad.data_ptr(), p.dtype, p.grad.dtype) for p in active)
-        if key != self._plan_key:
-            self._plan_key = None
-            self._build_plans(active)
-            self._plan_key = key
+        self._refresh_plans(active)
         lib = _lib.load()
-        bias1 = 1 - self.beta1**self.step_num
-        bias2 = 1 - self.beta2**self.step_num
+        bias1 = 1 - self.beta1**self._step_host
+        bias2 = 1 - self.beta2**self._step_host
         for plan in self._plans:
             with torch.cuda.device(plan.device):
                 st = lib.mamw_adamw_mt_step(
@@ -144,6 +161,42 @@ class HipAdamW:
                     self.beta1, self.beta2, self.weight_decay, self.eps,
                     _lib.stream_handle(plan.device))
             _lib.check(st, "mamw_adamw_mt_step")
+
+    @torch.no_grad()
+    def _step_amp(self, grad_scale: torch.Tensor | None, found_inf: torch.Tensor | None) -> None:
+        """One step driven by ``torch.amp.GradScaler`` with its tensors left on
+        the device, as torch's fused AdamW takes them (torch/optim/adam.py:865-899):
+        gradients divided by ``grad_scale``, no update where ``found_inf`` is
+        non-zero, and the step counter incremented before the launch and
+        decremented by ``found_inf`` after it, on the device.  Gradients are
+        read, not rewritten."""
+        active = [p for p in self.model_params if p.grad is not None]
+        if not active:  # nothing on the device to skip: the counter alone, on the host
+            if found_inf is None or float(found_inf) == 0.0:
+                self.step_num += 1
+            return
+        self._refresh_plans(active)
+        lib = _lib.load()
+        if not self._dev_steps:
+            start = float(self._step_host)
+            self._dev_steps = {plan.device: torch.full((), start, dtype=torch.float32, device=plan.device)
+                               for plan in self._plans}
+        for plan in self._plans:
+            dev = plan.device
+            if dev not in self._dev_steps:
+                self._dev_steps[dev] = next(iter(self._dev_steps.values())).to(dev)
+            counter = self._dev_steps[dev]
+            gs = grad_scale.to(dev, torch.float32, non_blocking=True) if grad_scale is not None else None
+            fi = found_inf.to(dev, torch.float32, non_blocking=True) if found_inf is not None else None
+            with torch.cuda.device(dev):
+                counter.add_(1.0)
+                st = lib.mamw_adamw_mt_step_amp(
+                    plan.table.data_ptr(), plan.n_tensors, plan.n_blocks, self.lr, self.beta1, self.beta2,
+                    self.weight_decay, self.eps, counter.data_ptr(), gs.data_ptr() if gs is not None else None,
+                    fi.data_ptr() if fi is not None else None, _lib.stream_handle(dev))
+                _lib.check(st, "mamw_adamw_mt_step_amp")
+                if fi is not None:
+                    counter.sub_(fi)
 
     def zero_grad(self, set_to_none: bool = False):
         """Resets gradients back to zero (the reference's behaviour), or to None

@@ -316,6 +316,17 @@ class HipMuon:
     @torch.no_grad()
     def step(self):
         """Optimizer step for the Muon optimizer."""
+        self._run(None, None)
+
+    @torch.no_grad()
+    def _step_amp(self, grad_scale: torch.Tensor | None, found_inf: torch.Tensor | None) -> None:
+        """One step driven by ``torch.amp.GradScaler`` with its tensors left on the
+        device: gradients divided by ``grad_scale``; where ``found_inf`` is
+        non-zero the momentum and the parameters are left untouched (no host
+        synchronisation).  Gradients are read, not rewritten."""
+        self._run(grad_scale, found_inf)
+
+    def _run(self, grad_scale: torch.Tensor | None, found_inf: torch.Tensor | None) -> None:
         active = [p for p in self.model_params if p.grad is not None]
         if not active:
             return
@@ -335,11 +346,27 @@ class HipMuon:
         lib = _lib.load()
         nest = int(bool(self.is_nesterov))
 
+        amp = grad_scale is not None or found_inf is not None
+        amp_ptrs: dict = {}  # device -> (grad_scale, found_inf) on that device, made before any fork
+        if amp:
+            for call in self._calls:
+                if call.device not in amp_ptrs:
+                    amp_ptrs[call.device] = tuple(
+                        t.to(call.device, torch.float32, non_blocking=True) if t is not None else None
+                        for t in (grad_scale, found_inf))
+
         def launch(call, ws, stream_handle):
             with torch.cuda.device(call.device):
-                st = lib.mamw_muon_step(call.arr, call.n, self.lr, self.weight_decay, self.beta, nest,
-                                        self.a, self.b, self.c, self.steps, self.eps, ws.data_ptr(),
-                                        ws.numel(), stream_handle)
+                if not amp:
+                    st = lib.mamw_muon_step(call.arr, call.n, self.lr, self.weight_decay, self.beta, nest,
+                                            self.a, self.b, self.c, self.steps, self.eps, ws.data_ptr(),
+                                            ws.numel(), stream_handle)
+                else:
+                    gs, fi = amp_ptrs[call.device]
+                    st = lib.mamw_muon_step_amp(call.arr, call.n, self.lr, self.weight_decay, self.beta, nest,
+                                                self.a, self.b, self.c, self.steps, self.eps, ws.data_ptr(),
+                                                ws.numel(), gs.data_ptr() if gs is not None else None,
+                                                fi.data_ptr() if fi is not None else None, stream_handle)
             _lib.check(st, "mamw_muon_step")
 
         if not self._concurrent:
@@ -359,6 +386,9 @@ class HipMuon:
             if key not in forked:
                 s.wait_stream(torch.cuda.current_stream(call.device))
                 self._ws[key].record_stream(s)
+                for t in amp_ptrs.get(call.device, ()):  # the scaler may drop its tensors after step()
+                    if t is not None:
+                        t.record_stream(s)
                 forked[key] = s
             launch(call, self._ws[key], s.cuda_stream)
         for (dev, _), s in forked.items():

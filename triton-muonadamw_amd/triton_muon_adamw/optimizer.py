@@ -163,6 +163,10 @@ class MuonAdamW(HipMuon, HipAdamW, torch.optim.Optimizer):
     between the two in both directions.
     """
 
+    # torch.amp.GradScaler passes grad_scale / found_inf to step() instead of
+    # unscaling in place and reading found_inf on the host.
+    _step_supports_amp_scaling = True
+
     def __init__(
         self,
         model_params: nn.Module | ParameterGroups,
@@ -230,15 +234,26 @@ class MuonAdamW(HipMuon, HipAdamW, torch.optim.Optimizer):
         """Apply one update with the AdamW branch, then the Muon branch.
 
         With ``closure``, the loss is re-evaluated (under ``torch.enable_grad``)
-        before the update and returned, as torch.optim does.
+        before the update and returned, as torch.optim does.  Under
+        ``torch.amp.GradScaler`` (``_step_supports_amp_scaling``) the scaler
+        hands over ``grad_scale`` and ``found_inf`` as device tensors
+        (torch/amp/grad_scaler.py:403-448): both branches unscale the gradients
+        in their kernels and skip a non-finite step on the device, with no host
+        synchronisation, as torch's fused AdamW does.
         """
         loss = None
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
         self._pull_groups()
-        self.adamw.step()
-        self.muon.step()
+        grad_scale = getattr(self, "grad_scale", None)
+        found_inf = getattr(self, "found_inf", None)
+        if grad_scale is None and found_inf is None:
+            self.adamw.step()
+            self.muon.step()
+        else:
+            self.adamw._step_amp(grad_scale, found_inf)
+            self.muon._step_amp(grad_scale, found_inf)
         return loss
 
     def zero_grad(self, set_to_none: bool = False) -> None:
