@@ -229,3 +229,35 @@ def test_grad_scaler_after_explicit_unscale(gpu):
         assert torch.equal(p.detach(), q.detach()), n
     assert all(torch.equal(t, u) for t, u in zip(_state(opt_a), _state(opt_b)))
     assert opt_a.adamw.step_num == 2
+
+
+@pytest.mark.filterwarnings("ignore:Synchronization debug mode is a prototype")
+def test_grad_scaler_step_does_not_synchronise(gpu):
+    """The device-side GradScaler path reads nothing back to the host: with
+    torch's sync debug mode set to "error", scaler.step / scaler.update raise
+    on a synchronising call (after a warm-up step that builds the plans).  The
+    gradients are new tensors every step, so the AdamW table is rebuilt and
+    uploaded each time, as under zero_grad(set_to_none=True).  (torch documents
+    the mode as a prototype that does not catch every synchronising call.)"""
+    a = _params(gpu)
+    opt = MuonAdamW(_split(a), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    scaler = torch.amp.GradScaler("cuda", init_scale=1024.0, growth_interval=1000)
+    scaler.scale(torch.ones((), device=gpu))
+    gen = torch.Generator(device=gpu).manual_seed(8)
+
+    def one_step():
+        for (_, p, _), gi in zip(a, _grads(a, gpu, gen)):
+            p.grad = gi * 1024.0
+        scaler.step(opt)
+        scaler.update()
+
+    one_step()
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        for _ in range(2):
+            one_step()
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    torch.cuda.synchronize()
+    assert opt.adamw.step_num == 3

@@ -72,12 +72,19 @@ class _DevicePlan:
             arr[i] = _lib.AdamWTensorEx(p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), p.numel(), flags, 0)
         nbytes = ctypes.c_size_t()
         _lib.check(lib.mamw_adamw_table_bytes(n, ctypes.byref(nbytes)), "mamw_adamw_table_bytes")
-        host = torch.empty(max(nbytes.value, 1), dtype=torch.uint8)
+        # Packed into pinned memory and copied without blocking the host: the
+        # table is rebuilt whenever a gradient tensor is replaced (every step
+        # under zero_grad(set_to_none=True)), and a pageable upload would
+        # synchronise each time.  torch's pinned-memory allocator keeps the
+        # staging block until the copy has completed.
+        host = torch.empty(max(nbytes.value, 1), dtype=torch.uint8, pin_memory=True)
         nblocks = ctypes.c_int64()
         _lib.check(lib.mamw_adamw_table_pack_ex(arr, n, host.data_ptr(), nbytes.value, ctypes.byref(nblocks)),
                    "mamw_adamw_table_pack_ex")
         self.device = device
-        self.table = host.to(device)
+        self.table = torch.empty(host.numel(), dtype=torch.uint8, device=device)
+        with torch.cuda.device(device):
+            self.table.copy_(host, non_blocking=True)
         self.n_tensors = n
         self.n_blocks = nblocks.value
 
