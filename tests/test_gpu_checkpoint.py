@@ -232,7 +232,7 @@ def test_grad_scaler_after_explicit_unscale(gpu):
 
 
 @pytest.mark.filterwarnings("ignore:Synchronization debug mode is a prototype")
-def test_grad_scaler_step_does_not_synchronise(gpu):
+def test_steps_do_not_synchronise(gpu):
     """The device-side GradScaler path reads nothing back to the host: with
     torch's sync debug mode set to "error", scaler.step / scaler.update raise
     on a synchronising call (after a warm-up step that builds the plans).  The
@@ -251,6 +251,11 @@ def test_grad_scaler_step_does_not_synchronise(gpu):
         scaler.step(opt)
         scaler.update()
 
+    def plain_step():
+        for (_, p, _), gi in zip(a, _grads(a, gpu, gen)):
+            p.grad = gi
+        opt.step()
+
     one_step()
     torch.cuda.synchronize()
     torch.cuda.set_sync_debug_mode("error")
@@ -261,3 +266,14 @@ def test_grad_scaler_step_does_not_synchronise(gpu):
         torch.cuda.set_sync_debug_mode("default")
     torch.cuda.synchronize()
     assert opt.adamw.step_num == 3
+    # the plain step (no scaler) does not synchronise either
+    plain_step()
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        for _ in range(2):
+            plain_step()
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    torch.cuda.synchronize()
+    assert opt.adamw.step_num == 6
