@@ -277,3 +277,38 @@ def test_steps_do_not_synchronise(gpu):
         torch.cuda.set_sync_debug_mode("default")
     torch.cuda.synchronize()
     assert opt.adamw.step_num == 6
+
+
+@pytest.mark.parametrize("in_order", [True, False])
+def test_steps_under_a_side_stream(gpu, in_order):
+    """Steps taken with a side stream current (every other step), with new
+    gradient tensors each step so that the AdamW table is re-packed and the
+    launch groups rebuilt while earlier launches may still be queued, give the
+    same parameters bit for bit as steps on the default stream.  ``in_order``
+    runs the Muon shape classes in order on the caller's stream (the path of
+    large steps) instead of on forked side streams."""
+    a, b = _params(gpu), _params(gpu)
+    opt_a = MuonAdamW(_split(a), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    opt_b = MuonAdamW(_split(b), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    if in_order:
+        opt_a.muon.concurrent_flops_limit = opt_b.muon.concurrent_flops_limit = 0.0
+    gen = torch.Generator(device=gpu).manual_seed(12)
+    side = torch.cuda.Stream(device=gpu)
+    main = torch.cuda.current_stream(gpu)
+    for k in range(4):
+        grads = _grads(a, gpu, gen)
+        _set(a, grads)
+        _set(b, grads)
+        opt_a.step()
+        if k % 2:
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                opt_b.step()
+            main.wait_stream(side)
+        else:
+            opt_b.step()
+        del grads
+    torch.cuda.synchronize()
+    assert opt_b.muon._concurrent is not in_order
+    for (n, p, _), (_, q, _) in zip(a, b):
+        assert torch.equal(p, q), n

@@ -88,6 +88,15 @@ class _DevicePlan:
         self.n_tensors = n
         self.n_blocks = nblocks.value
 
+    def launch_stream(self) -> int:
+        """Handle of the current stream, on which the table is about to be
+        read.  The table was allocated on the stream current when it was packed;
+        recording this one keeps torch's allocator from reusing the table's
+        memory, once the plan is replaced, before the launch has run."""
+        s = torch.cuda.current_stream(self.device)
+        self.table.record_stream(s)
+        return s.cuda_stream
+
 
 class HipAdamW:
     """AdamW over a list of parameters, one gfx950 kernel launch per step."""
@@ -165,8 +174,7 @@ class HipAdamW:
             with torch.cuda.device(plan.device):
                 st = lib.mamw_adamw_mt_step(
                     plan.table.data_ptr(), plan.n_tensors, plan.n_blocks, self.lr, bias1, bias2,
-                    self.beta1, self.beta2, self.weight_decay, self.eps,
-                    _lib.stream_handle(plan.device))
+                    self.beta1, self.beta2, self.weight_decay, self.eps, plan.launch_stream())
             _lib.check(st, "mamw_adamw_mt_step")
 
     @torch.no_grad()
@@ -200,7 +208,7 @@ class HipAdamW:
                 st = lib.mamw_adamw_mt_step_amp(
                     plan.table.data_ptr(), plan.n_tensors, plan.n_blocks, self.lr, self.beta1, self.beta2,
                     self.weight_decay, self.eps, counter.data_ptr(), gs.data_ptr() if gs is not None else None,
-                    fi.data_ptr() if fi is not None else None, _lib.stream_handle(dev))
+                    fi.data_ptr() if fi is not None else None, plan.launch_stream())
                 _lib.check(st, "mamw_adamw_mt_step_amp")
                 if fi is not None:
                     counter.sub_(fi)

@@ -371,7 +371,9 @@ class HipMuon:
 
         if not self._concurrent:
             for call in self._calls:
-                launch(call, self._ws[call.device], _lib.stream_handle(call.device))
+                ws, cur = self._ws[call.device], torch.cuda.current_stream(call.device)
+                ws.record_stream(cur)  # allocated under the stream current when the plan was built
+                launch(call, ws, cur.cuda_stream)
             return
         # One side stream per shape class: each waits for the caller's current
         # stream, runs its class's launches in order, and the current stream
