@@ -312,3 +312,66 @@ def test_steps_under_a_side_stream(gpu, in_order):
     assert opt_b.muon._concurrent is not in_order
     for (n, p, _), (_, q, _) in zip(a, b):
         assert torch.equal(p, q), n
+
+
+@pytest.mark.parametrize("in_order", [True, False])
+def test_graph_captured_step_replays_like_eager_steps(gpu, in_order):
+    """``capturable=True``: one eager step, then a step captured with
+    ``torch.cuda.graph`` and replayed three times (new gradients copied into the
+    static ``.grad`` tensors before each replay, eager steps of a twin
+    optimizer and a synchronisation between replays) gives the parameters,
+    moments and momentum of four eager steps bit for bit, each replay checked;
+    the device step counter reads 4.  ``in_order``: Muon shape classes in
+    order on the capture stream, else forked onto side streams inside the
+    graph."""
+    a, b = _params(gpu), _params(gpu)
+    opt_a = MuonAdamW(_split(a), muon_config=MC, adam_config=AC, parameter_split="explicit", capturable=True)
+    opt_b = MuonAdamW(_split(b), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    if in_order:
+        opt_a.muon.concurrent_flops_limit = opt_b.muon.concurrent_flops_limit = 0.0
+    gen = torch.Generator(device=gpu).manual_seed(13)
+    grads = _grads(a, gpu, gen)
+    _set(a, grads)
+    _set(b, grads)
+    opt_a.step()
+    opt_b.step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        opt_a.step()
+    assert opt_a.param_groups[0]["params"][0].grad is not None
+    for k in range(3):
+        grads = _grads(a, gpu, gen)
+        for (_, p, _), g in zip(a, grads):
+            p.grad.copy_(g)
+        graph.replay()
+        _set(b, grads)
+        opt_b.step()
+        torch.cuda.synchronize()
+        for (n, p, _), (_, q, _) in zip(a, b):
+            assert torch.equal(p, q), (k, n)
+    assert opt_b.muon._concurrent is not in_order
+    for (n, p, br), (_, q, _) in zip(a, b):
+        if br == "adam":
+            assert torch.equal(opt_a.adamw.m[p], opt_b.adamw.m[q]) and torch.equal(opt_a.adamw.v[p], opt_b.adamw.v[q]), n
+        else:
+            assert torch.equal(opt_a.muon.momentum[p], opt_b.muon.momentum[q]), n
+    assert opt_a.adamw.step_num == 4 and opt_b.adamw.step_num == 4
+    assert opt_a.adamw.state_dict()["param_groups"][0]["capturable"] is True
+
+
+@pytest.mark.filterwarnings("ignore:The CUDA Graph is empty")
+def test_capture_refuses_a_plan_change(gpu):
+    """A step whose launch plan would be built during capture (no eager step
+    yet) raises instead of recording pointers that a replay could not keep."""
+    a = _params(gpu)
+    opt = MuonAdamW(_split(a), muon_config=MC, adam_config=AC, parameter_split="explicit", capturable=True)
+    _set(a, _grads(a, gpu, torch.Generator(device=gpu).manual_seed(14)))
+    graph = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="during graph capture"):
+        with torch.cuda.graph(graph):
+            opt.step()
+    torch.cuda.synchronize()
+    opt.step()  # eager steps still work after the failed capture
+    torch.cuda.synchronize()
+    assert opt.adamw.step_num == 1

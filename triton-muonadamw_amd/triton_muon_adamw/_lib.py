@@ -176,6 +176,16 @@ def require_gpu_tensor(t: torch.Tensor, name: str) -> None:
             "(there is no CPU path)")
 
 
+def check_not_capturing(branch: str) -> None:
+    """Launch plans and device step counters are made by eager steps only: a
+    graph replays the pointers, scalars and table upload recorded at capture."""
+    if torch.cuda.is_available() and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(
+            f"{branch}: a launch plan or step counter would be created during graph capture; take one eager "
+            "step first and keep the .grad tensors static between capture and replay (copy new gradients "
+            "into them)")
+
+
 def stream_handle(device: torch.device) -> int:
     """hipStream_t of torch's current stream on ``device`` (0 = null stream)."""
     return torch.cuda.current_stream(device).cuda_stream

@@ -99,7 +99,12 @@ class _DevicePlan:
 
 
 class HipAdamW:
-    """AdamW over a list of parameters, one gfx950 kernel launch per step."""
+    """AdamW over a list of parameters, one gfx950 kernel launch per step.
+
+    ``capturable=True`` (as in torch.optim.AdamW) keeps the step counter on the
+    device from the first step on, so that a step captured in a CUDA/HIP graph
+    advances it, and forms the bias corrections from it, at every replay.
+    """
 
     def __init__(
         self,
@@ -108,7 +113,10 @@ class HipAdamW:
         betas: tuple[float, float] = (0.9, 0.999),
         weight_decay=1e-2,
         eps=1e-7,
+        *,
+        capturable: bool = False,
     ):
+        self.capturable = bool(capturable)
         self.model_params = list(params)
         self.beta1 = betas[0]
         self.beta2 = betas[1]
@@ -155,6 +163,7 @@ class HipAdamW:
     def _refresh_plans(self, active: list[nn.Parameter]) -> None:
         key = tuple((id(p), p.data_ptr(), p.grad.data_ptr(), p.dtype, p.grad.dtype) for p in active)
         if key != self._plan_key:
+            _lib.check_not_capturing("AdamW")
             self._plan_key = None
             self._build_plans(active)
             self._plan_key = key
@@ -162,6 +171,9 @@ class HipAdamW:
     @torch.no_grad()
     def step(self):
         """Performs one iteration of the AdamW optimizer step."""
+        if self.capturable:
+            self._step_amp(None, None)
+            return
         self.step_num += 1
         active = [p for p in self.model_params if p.grad is not None]
         if not active:
@@ -186,13 +198,19 @@ class HipAdamW:
         decremented by ``found_inf`` after it, on the device.  Gradients are
         read, not rewritten."""
         active = [p for p in self.model_params if p.grad is not None]
-        if not active:  # nothing on the device to skip: the counter alone, on the host
-            if found_inf is None or float(found_inf) == 0.0:
-                self.step_num += 1
+        if not active:  # nothing to update: the counter alone
+            if self._dev_steps:
+                for c in self._dev_steps.values():
+                    c.add_(1.0)
+                    if found_inf is not None:
+                        c.sub_(found_inf.to(c.device, torch.float32, non_blocking=True))
+            elif found_inf is None or float(found_inf) == 0.0:
+                self._step_host += 1
             return
         self._refresh_plans(active)
         lib = _lib.load()
         if not self._dev_steps:
+            _lib.check_not_capturing("AdamW")
             start = float(self._step_host)
             self._dev_steps = {plan.device: torch.full((), start, dtype=torch.float32, device=plan.device)
                                for plan in self._plans}
@@ -238,7 +256,7 @@ class HipAdamW:
                             "exp_avg_sq": self.v[p]}
         group = {"lr": self.lr, "betas": (self.beta1, self.beta2), "eps": self.eps,
                  "weight_decay": self.weight_decay, "amsgrad": False, "maximize": False, "foreach": None,
-                 "capturable": False, "differentiable": False, "fused": True, "decoupled_weight_decay": True,
+                 "capturable": self.capturable, "differentiable": False, "fused": True, "decoupled_weight_decay": True,
                  "params": list(range(len(self.model_params)))}
         return {"state": state, "param_groups": [group]}
 

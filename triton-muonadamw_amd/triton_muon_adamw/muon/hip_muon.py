@@ -333,6 +333,7 @@ class HipMuon:
         key = (self.adjust_lr_fn, self.steps,
                tuple((id(p), p.data_ptr(), p.grad.data_ptr(), p.dtype, p.grad.dtype) for p in active))
         if key != self._plan_key:
+            _lib.check_not_capturing("Muon")
             self._plan_key = None
             self._build_calls(active)
             self._plan_key = key

@@ -161,6 +161,13 @@ class MuonAdamW(HipMuon, HipAdamW, torch.optim.Optimizer):
     and ``state_dict()`` carries the optimizer state (moments, step, momentum)
     in the format of ``PyTorchMuonAdamW.state_dict()``, so checkpoints move
     between the two in both directions.
+
+    ``capturable=True`` (keyword only, as torch.optim.AdamW's flag) lets a step
+    be captured in a CUDA/HIP graph (``torch.cuda.graph``) after one eager step:
+    the AdamW step counter lives on the device and advances at every replay.
+    A replay reuses the launches recorded at capture: the parameter, gradient
+    and state tensors (copy new gradients into the same ``.grad`` tensors) and
+    the hyperparameters of that moment (learning rates included).
     """
 
     # torch.amp.GradScaler passes grad_scale / found_inf to step() instead of
@@ -173,6 +180,8 @@ class MuonAdamW(HipMuon, HipAdamW, torch.optim.Optimizer):
         muon_config: MuonConfig = MuonConfig(),  # noqa: B008
         adam_config: AdamConfig = AdamConfig(),  # noqa: B008
         parameter_split: Literal["auto", "explicit"] = "auto",
+        *,
+        capturable: bool = False,
     ) -> None:
         adam_params, muon_params = split_parameters(model_params, parameter_split)
         self.adamw = HipAdamW(
@@ -181,6 +190,7 @@ class MuonAdamW(HipMuon, HipAdamW, torch.optim.Optimizer):
             betas=adam_config.betas,
             weight_decay=adam_config.weight_decay,
             eps=adam_config.eps,
+            capturable=capturable,
         )
         self.muon = HipMuon(
             params=muon_params,
