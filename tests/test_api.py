@@ -203,3 +203,23 @@ def test_adamw_step_counter_host_and_device_views():
     opt.step_num = 3
     assert opt.step_num == 3 and opt._dev_steps == {}
     assert MuonAdamW._step_supports_amp_scaling
+
+
+def test_capturable_flag():
+    """``capturable`` is keyword-only, off by default, passed to the AdamW
+    branch and reported in its state dict as torch.optim.AdamW does; a step
+    with no gradients keeps a device-side counter on the device."""
+    from triton_muon_adamw.adamw import HipAdamW
+
+    lin = nn.Linear(8, 8)
+    groups = {"adam": [lin.bias], "muon": [lin.weight]}
+    assert MuonAdamW(groups, parameter_split="explicit").adamw.capturable is False
+    opt = MuonAdamW(groups, parameter_split="explicit", capturable=True)
+    assert opt.adamw.capturable is True
+    assert opt.adamw.state_dict()["param_groups"][0]["capturable"] is True
+    with pytest.raises(TypeError):
+        MuonAdamW(groups, MuonConfig(), AdamConfig(), "explicit", True)
+    a = HipAdamW([nn.Parameter(torch.zeros(4))], capturable=True)
+    a._dev_steps = {torch.device("cpu"): torch.tensor(2.0)}  # as the first capturable step leaves it
+    a.step()  # no gradient: the counter alone advances, where it lives
+    assert a._dev_steps and a.step_num == 3
