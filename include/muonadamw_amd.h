@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MAMW_ABI_VERSION 3
+#define MAMW_ABI_VERSION 4
 
 /* ---- status codes -------------------------------------------------------- */
 #define MAMW_OK             0
@@ -105,7 +105,8 @@ int mamw_adamw_tensor_step(float* param, const float* grad, float* exp_avg,
 /* Multi-tensor AdamW: every tensor of a step in ONE launch.  Replaces the
  * per-parameter launch loop of TritonAdamW.step (triton_adam.py:132-153).
  *
- * 1. mamw_adamw_table_bytes: size of the packed table for n_tensors.
+ * 1. mamw_adamw_table_bytes: size of the packed table for n_tensors (one
+ *    64-byte record per tensor plus one that mamw_adamw_mt_step_amp writes).
  * 2. mamw_adamw_table_pack (host only, no HIP call): validates the tensors and
  *    packs the table into host memory; returns the launch's block count.
  * 3. The caller copies the table to device memory (16-byte aligned) and keeps
@@ -132,7 +133,10 @@ int mamw_adamw_mt_step(const void* device_table, int n_tensors,
  *   step:       device fp32 step counter, already incremented for this step;
  *               the bias corrections are 1 - beta^step, formed on the device
  *               in double from the double betas and rounded to fp32, as the
- *               host forms them for mamw_adamw_mt_step.  Required.
+ *               host forms them for mamw_adamw_mt_step, by a one-wave kernel
+ *               launched first that stores them in the table's trailing
+ *               record (so calls sharing one table must not overlap).
+ *               Required.
  *   grad_scale: device fp32; every gradient is divided by it.  NULL: none.
  *   found_inf:  device fp32; non-zero skips the update (parameters and
  *               moments untouched).  NULL: never skipped.

@@ -37,7 +37,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_strerror():
     lib = _lib.load()
-    assert lib.mamw_abi_version() == 3
+    assert lib.mamw_abi_version() == 4
     for code in (OK, NULL, COUNT, NUMEL, SHAPE, ALIGN, WS, HYPER, TABLE, ALIAS):
         msg = lib.mamw_strerror(code).decode()
         assert msg and msg != "unknown status"
@@ -58,7 +58,7 @@ def _pack(tensors):
     arr = (_lib.AdamWTensor * max(n, 1))(*tensors)
     nbytes = ctypes.c_size_t()
     assert lib.mamw_adamw_table_bytes(n, ctypes.byref(nbytes)) == OK
-    assert nbytes.value == 64 * n
+    assert nbytes.value == 64 * (n + 1)  # + the record the device-counter step writes
     buf = (ctypes.c_uint8 * max(nbytes.value, 1))()
     blocks = ctypes.c_int64(-1)
     st = lib.mamw_adamw_table_pack(arr, n, buf, nbytes.value, ctypes.byref(blocks))
@@ -83,9 +83,9 @@ def _pack_ex(entries):
     lib = _lib.load()
     n = len(entries)
     arr = (_lib.AdamWTensorEx * max(n, 1))(*entries)
-    buf = (ctypes.c_uint8 * max(64 * n, 1))()
+    buf = (ctypes.c_uint8 * (64 * (n + 1)))()
     blocks = ctypes.c_int64(-1)
-    st = lib.mamw_adamw_table_pack_ex(arr, n, buf, 64 * n, ctypes.byref(blocks))
+    st = lib.mamw_adamw_table_pack_ex(arr, n, buf, 64 * (n + 1), ctypes.byref(blocks))
     return st, bytes(buf), blocks.value
 
 

@@ -22,12 +22,11 @@ struct AdamWConsts {
     float omb1, omb2, decay;  // 1-beta1, 1-beta2, 1-lr*weight_decay (fp32, as the reference)
     // Gradient-scaler step (all NULL otherwise): gradients are divided by
     // *grad_scale; a non-zero *found_inf skips the update; the bias
-    // corrections come from the device step counter *step, in double from the
-    // double betas, as the host forms them from its own counter.
+    // corrections are read from bias[0..1], written just before by
+    // adamw_bias_kernel from the device step counter.
     const float* grad_scale;
     const float* found_inf;
-    const float* step;
-    double beta1d, beta2d;
+    const float* bias;
     float gs;     // *grad_scale, read by the kernel
     int scaled;   // grad_scale != NULL
 };
@@ -43,8 +42,7 @@ __host__ AdamWConsts make_consts(const AdamWScalars& s) {
     c.omb1 = 1.0f - s.beta1;
     c.omb2 = 1.0f - s.beta2;
     c.decay = 1.0f - s.lr * s.weight_decay;
-    c.grad_scale = c.found_inf = c.step = nullptr;
-    c.beta1d = c.beta2d = 0.0;
+    c.grad_scale = c.found_inf = c.bias = nullptr;
     c.gs = 1.0f;
     c.scaled = 0;
     return c;
@@ -53,10 +51,9 @@ __host__ AdamWConsts make_consts(const AdamWScalars& s) {
 // Per-block set-up of a gradient-scaler step: false when the step is skipped.
 __device__ __forceinline__ bool adamw_prepare(AdamWConsts& c) {
     if (c.found_inf && *c.found_inf != 0.0f) return false;
-    if (c.step) {
-        const double st = double(*c.step);
-        c.bias1 = float(1.0 - pow(c.beta1d, st));
-        c.bias2 = float(1.0 - pow(c.beta2d, st));
+    if (c.bias) {
+        c.bias1 = c.bias[0];
+        c.bias2 = c.bias[1];
     }
     if (c.grad_scale) {
         c.gs = *c.grad_scale;
@@ -253,13 +250,13 @@ extern "C" int mamw_adamw_tensor_step(float* param, const float* grad, float* ex
                                       float eps, mamw_stream_t stream) {
     mamw_adamw_tensor t{param, grad, exp_avg, exp_avg_sq, numel};
     int64_t blocks = 0;
-    AdamWRec r;
-    int st = adamw_table_pack(&t, 1, &r, sizeof(r), &blocks);
+    AdamWRec r[2];  // a packed table of one tensor (the trailing record is unused here)
+    int st = adamw_table_pack(&t, 1, r, sizeof(r), &blocks);
     if (st != MAMW_OK) return st;
     if (blocks == 0) return MAMW_OK;
     AdamWScalars s{lr, bias1, bias2, beta1, beta2, weight_decay, eps};
     return int(launch(K_ADAMW_ONE, 0, 0.0, 28.0 * double(numel), adamw_one_kernel, dim3(unsigned(blocks)),
-                      dim3(kAdamWThreads), static_cast<hipStream_t>(stream), r, make_consts(s)));
+                      dim3(kAdamWThreads), static_cast<hipStream_t>(stream), r[0], make_consts(s)));
 }
 
 extern "C" int mamw_adamw_table_bytes(int n_tensors, size_t* bytes) {
@@ -277,6 +274,18 @@ extern "C" int mamw_adamw_table_pack_ex(const mamw_adamw_tensor_ex* tensors, int
 }
 
 namespace {
+// The bias corrections of a device-counter step, once per launch (rather than
+// in every wave of the update): 1 - beta^step in double from the double
+// betas, rounded to fp32, as the host forms them from its own counter.
+__global__ __launch_bounds__(64) void adamw_bias_kernel(const float* __restrict__ step, double beta1,
+                                                        double beta2, float* __restrict__ bias) {
+    if (threadIdx.x == 0) {
+        const double st = double(*step);
+        bias[0] = float(1.0 - pow(beta1, st));
+        bias[1] = float(1.0 - pow(beta2, st));
+    }
+}
+
 int adamw_mt_launch(const void* device_table, int n_tensors, int64_t n_blocks, const AdamWConsts& c,
                     mamw_stream_t stream) {
     if (n_tensors < 0 || n_tensors > kMaxTensors) return MAMW_ERR_COUNT;
@@ -303,12 +312,20 @@ extern "C" int mamw_adamw_mt_step_amp(const void* device_table, int n_tensors, i
                                       const float* step, const float* grad_scale, const float* found_inf,
                                       mamw_stream_t stream) {
     if (!step) return MAMW_ERR_NULL;
+    if (n_tensors < 0 || n_tensors > kMaxTensors) return MAMW_ERR_COUNT;
+    if (n_blocks <= 0) return n_blocks < 0 ? MAMW_ERR_NUMEL : MAMW_OK;
+    if (n_tensors == 0) return MAMW_ERR_COUNT;
+    if (!device_table) return MAMW_ERR_NULL;
+    if (reinterpret_cast<uintptr_t>(device_table) % 16) return MAMW_ERR_ALIGN;
     AdamWScalars s{lr, 1.0f, 1.0f, float(beta1), float(beta2), weight_decay, eps};
     AdamWConsts c = make_consts(s);
-    c.step = step;
+    // The table's trailing record (after n_tensors records) holds the two corrections.
+    float* bias = reinterpret_cast<float*>(static_cast<AdamWRec*>(const_cast<void*>(device_table)) + n_tensors);
+    c.bias = bias;
     c.grad_scale = grad_scale;
     c.found_inf = found_inf;
-    c.beta1d = beta1;
-    c.beta2d = beta2;
+    const int st = int(launch(K_ADAMW_BIAS, 0, 0.0, 0.0, adamw_bias_kernel, dim3(1), dim3(64),
+                              static_cast<hipStream_t>(stream), step, beta1, beta2, bias));
+    if (st != 0) return st;
     return adamw_mt_launch(device_table, n_tensors, n_blocks, c, stream);
 }

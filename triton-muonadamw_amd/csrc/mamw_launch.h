@@ -27,6 +27,7 @@ enum KernelId : int32_t {
     K_NS_UPDATE,
     K_NS_APPLY,
     K_TRANSPOSE,
+    K_ADAMW_BIAS,
     K_COUNT
 };
 

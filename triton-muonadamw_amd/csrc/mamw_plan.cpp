@@ -44,7 +44,7 @@ int adamw_validate_tensor(const mamw_adamw_tensor_ex& t) {
 int adamw_table_bytes(int n_tensors, size_t* bytes) {
     if (!bytes) return MAMW_ERR_NULL;
     if (n_tensors < 0 || n_tensors > kMaxTensors) return MAMW_ERR_COUNT;
-    *bytes = size_t(n_tensors) * sizeof(AdamWRec);
+    *bytes = size_t(n_tensors + 1) * sizeof(AdamWRec);  // + the record the device-counter step writes
     return MAMW_OK;
 }
 
@@ -53,7 +53,7 @@ int adamw_table_pack_ex(const mamw_adamw_tensor_ex* tensors, int n_tensors, void
     if (!n_blocks) return MAMW_ERR_NULL;
     if (n_tensors < 0 || n_tensors > kMaxTensors) return MAMW_ERR_COUNT;
     if (n_tensors > 0 && (!tensors || !host_table)) return MAMW_ERR_NULL;
-    if (table_bytes < size_t(n_tensors) * sizeof(AdamWRec)) return MAMW_ERR_TABLE;
+    if (n_tensors > 0 && table_bytes < size_t(n_tensors + 1) * sizeof(AdamWRec)) return MAMW_ERR_TABLE;
     AdamWRec* rec = static_cast<AdamWRec*>(host_table);
     int64_t blocks = 0;
     for (int i = 0; i < n_tensors; ++i) {
@@ -77,6 +77,7 @@ int adamw_table_pack_ex(const mamw_adamw_tensor_ex* tensors, int n_tensors, void
         blocks += (t.numel + kAdamWChunk - 1) / kAdamWChunk;
         if (blocks > int64_t(0x7fffffff)) return MAMW_ERR_NUMEL;  // grid.x limit
     }
+    if (n_tensors > 0) memset(&rec[n_tensors], 0, sizeof(AdamWRec));  // written by the device-counter step
     *n_blocks = blocks;
     return MAMW_OK;
 }
@@ -86,7 +87,7 @@ int adamw_table_pack(const mamw_adamw_tensor* tensors, int n_tensors, void* host
     if (!n_blocks) return MAMW_ERR_NULL;
     if (n_tensors < 0 || n_tensors > kMaxTensors) return MAMW_ERR_COUNT;
     if (n_tensors > 0 && (!tensors || !host_table)) return MAMW_ERR_NULL;
-    if (table_bytes < size_t(n_tensors) * sizeof(AdamWRec)) return MAMW_ERR_TABLE;
+    if (n_tensors > 0 && table_bytes < size_t(n_tensors + 1) * sizeof(AdamWRec)) return MAMW_ERR_TABLE;
     // fp32 entries are packed one at a time through the general path (no allocation).
     AdamWRec* rec = static_cast<AdamWRec*>(host_table);
     int64_t blocks = 0;
@@ -94,7 +95,7 @@ int adamw_table_pack(const mamw_adamw_tensor* tensors, int n_tensors, void* host
         const mamw_adamw_tensor& t = tensors[i];
         const mamw_adamw_tensor_ex e{t.param, t.grad, t.exp_avg, t.exp_avg_sq, t.numel, 0, 0};
         int64_t nb = 0;
-        int st = adamw_table_pack_ex(&e, 1, &rec[i], sizeof(AdamWRec), &nb);
+        int st = adamw_table_pack_ex(&e, 1, &rec[i], table_bytes - size_t(i) * sizeof(AdamWRec), &nb);
         if (st != MAMW_OK) return st;
         rec[i].block_begin = blocks;
         blocks += nb;

@@ -43,7 +43,7 @@ const char* const kNames[K_COUNT] = {
     "adamw_mt_kernel", "adamw_one_kernel", "muon_prep_kernel", "muon_norm_kernel", "muon_apply0_kernel",
     "muon_scale_kernel",
     "ns_gemm_kernel:gram", "ns_gemm_kernel:poly", "ns_gemm_kernel:update", "ns_gemm_kernel:apply",
-    "transpose_bf16_kernel",
+    "transpose_bf16_kernel", "adamw_bias_kernel",
 };
 
 }  // namespace

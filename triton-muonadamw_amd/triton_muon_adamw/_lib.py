@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libmuonadamw_amd.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 MUON_MAX_BATCH = 32
 BF16_PARAM = 0x1  # MAMW_BF16_PARAM
 BF16_GRAD = 0x2   # MAMW_BF16_GRAD
