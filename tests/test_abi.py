@@ -255,3 +255,18 @@ def test_profiler_without_launches():
     lib = _lib.load()
     assert lib.mamw_prof_kernel_name(0).decode() == "adamw_mt_kernel"
     assert lib.mamw_prof_kernel_name(99).decode() == "unknown"
+
+
+def test_adamw_amp_launch_validation_before_hip():
+    """mamw_adamw_mt_step_amp rejects its arguments on the host before its
+    first launch (the bias-correction kernel), so nothing here touches a GPU."""
+    lib = _lib.load()
+    step = 1 << 40  # never dereferenced: every call below is rejected or launches nothing
+    hp = (3e-4, 0.9, 0.95, 0.1, 1e-8)
+    assert lib.mamw_adamw_mt_step_amp(1 << 40, 1, 5, *hp, None, None, None, None) == NULL
+    assert lib.mamw_adamw_mt_step_amp(None, 1, 5, *hp, step, None, None, None) == NULL
+    assert lib.mamw_adamw_mt_step_amp(1 << 40 | 8, 1, 5, *hp, step, None, None, None) == ALIGN
+    assert lib.mamw_adamw_mt_step_amp(1 << 40, 1, -1, *hp, step, None, None, None) == NUMEL
+    assert lib.mamw_adamw_mt_step_amp(1 << 40, 0, 5, *hp, step, None, None, None) == COUNT
+    assert lib.mamw_adamw_mt_step_amp(1 << 40, -1, 5, *hp, step, None, None, None) == COUNT
+    assert lib.mamw_adamw_mt_step_amp(None, 0, 0, *hp, step, None, None, None) == OK  # nothing to do
