@@ -140,8 +140,11 @@ int mamw_adamw_mt_step(const void* device_table, int n_tensors,
  *   grad_scale: device fp32; every gradient is divided by it.  NULL: none.
  *   found_inf:  device fp32; non-zero skips the update (parameters and
  *               moments untouched).  NULL: never skipped.
- * The caller decrements *step by *found_inf afterwards, as torch does.      */
-int mamw_adamw_mt_step_amp(const void* device_table, int n_tensors,
+ * The caller decrements *step by *found_inf afterwards, as torch does.
+ * device_table must be writable device memory (the trailing record is
+ * written); every argument is validated, n_blocks included, before the first
+ * launch.                                                                   */
+int mamw_adamw_mt_step_amp(void* device_table, int n_tensors,
                            int64_t n_blocks, float lr, double beta1,
                            double beta2, float weight_decay, float eps,
                            const float* step, const float* grad_scale,
@@ -204,7 +207,9 @@ int mamw_muon_step_amp(const mamw_muon_matrix* mats, int batch, double lr,
 
 /* ==== Newton-Schulz building blocks (batched, bf16, fp32 accumulate) ======== *
  * Operate on `batch` contiguous zero-padded row-major matrices.  m and n must
- * be multiples of 128 and k a multiple of 64; the Python mirrors pad.          */
+ * be multiples of 128 and k a multiple of 64; the Python mirrors pad.  An
+ * output whose byte range (over the whole batch) overlaps a buffer the same
+ * call reads, or the other output, is rejected with MAMW_ERR_ALIAS.            */
 
 /* A = X X^T  (X: m x k, A: m x m).  Replaces solve_ns_kernel_1
  * (triton_muon.py:95-117).  Only tiles on or above the diagonal are computed;
@@ -218,13 +223,15 @@ int mamw_ns_poly(const uint16_t* A, uint16_t* B, int batch, int64_t m,
                  float b, float c, mamw_stream_t stream);
 
 /* out = a X + B X  (B: m x m symmetric, X: m x n).  Replaces solve_ns_kernel_3
- * (triton_muon.py:281-310).  XT must hold X^T (n x m); out may equal X; out_t,
- * if not NULL, receives out^T (n x m) and must not overlap XT.                 */
+ * (triton_muon.py:281-310).  XT must hold X^T (n x m); X itself is not read
+ * (out may equal X); out must not overlap B or XT; out_t, if not NULL,
+ * receives out^T (n x m) and must not overlap B, XT or out.                   */
 int mamw_ns_update(const uint16_t* B, const uint16_t* X, const uint16_t* XT,
                    uint16_t* out, uint16_t* out_t, int batch, int64_t m,
                    int64_t n, float a, mamw_stream_t stream);
 
-/* dst = src^T for `batch` bf16 matrices (src rows x cols, dst cols x rows). */
+/* dst = src^T for `batch` bf16 matrices (src rows x cols, dst cols x rows);
+ * src and dst must not overlap.                                              */
 int mamw_transpose_bf16(const uint16_t* src, uint16_t* dst, int batch,
                         int64_t rows, int64_t cols, mamw_stream_t stream);
 

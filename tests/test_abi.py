@@ -245,7 +245,30 @@ def test_ns_blocks_validation():
     assert lib.mamw_ns_update(1 << 40, 2 << 40, 3 << 40, 4 << 40, 3 << 40, 1, 128, 256, 3.44, None) == ALIAS
     assert lib.mamw_ns_update(1 << 40, 2 << 40, 3 << 40, 4 << 40, None, 1, 128, 200, 3.44, None) == SHAPE
     assert lib.mamw_transpose_bf16(1 << 40, 1 << 40, 1, 4, 4, None) == ALIAS
+    assert lib.mamw_transpose_bf16(1 << 40, (1 << 40) + 16, 1, 4, 4, None) == ALIAS  # partial overlap
     assert lib.mamw_transpose_bf16(1 << 40, 2 << 40, 0, 4, 4, None) == COUNT
+
+
+def test_ns_blocks_reject_overlapping_buffers():
+    """Operands, epilogue sources and outputs of the standalone GEMMs that would
+    race are rejected by byte-range overlap before any HIP call."""
+    lib = _lib.load()
+    m, k = 256, 512
+    X = 1 << 40
+    # Gram: A inside X, or X starting inside A
+    assert lib.mamw_ns_gram(X, X + 2 * m * 64, 1, m, k, None) == ALIAS
+    assert lib.mamw_ns_gram(X + 1024, X, 1, m, k, None) == ALIAS
+    # polynomial: B overlapping A partly
+    assert lib.mamw_ns_poly(X, X + 2 * m * m - 16, 1, m, -4.775, 2.03, None) == ALIAS
+    assert lib.mamw_ns_poly(X, X + 2 * 2 * m * m - 16, 2, m, -4.775, 2.03, None) == ALIAS  # batch extent
+    # update: out over B, out over XT, out_t over B / XT / out
+    n = 512
+    B, XT, out, out_t = 1 << 40, 2 << 40, 3 << 40, 4 << 40
+    assert lib.mamw_ns_update(B, out, XT, B + 64, None, 1, m, n, 3.44, None) == ALIAS
+    assert lib.mamw_ns_update(B, out, XT, XT + 2 * n * m - 16, None, 1, m, n, 3.44, None) == ALIAS
+    assert lib.mamw_ns_update(B, out, XT, out, B, 1, m, n, 3.44, None) == ALIAS
+    assert lib.mamw_ns_update(B, out, XT, out, XT + 4096, 1, m, n, 3.44, None) == ALIAS
+    assert lib.mamw_ns_update(B, out, XT, out, out + 2 * m * n - 16, 1, m, n, 3.44, None) == ALIAS
 
 
 def test_profiler_without_launches():
@@ -270,3 +293,6 @@ def test_adamw_amp_launch_validation_before_hip():
     assert lib.mamw_adamw_mt_step_amp(1 << 40, 0, 5, *hp, step, None, None, None) == COUNT
     assert lib.mamw_adamw_mt_step_amp(1 << 40, -1, 5, *hp, step, None, None, None) == COUNT
     assert lib.mamw_adamw_mt_step_amp(None, 0, 0, *hp, step, None, None, None) == OK  # nothing to do
+    # beyond the grid limit: rejected before the bias kernel would be launched
+    assert lib.mamw_adamw_mt_step_amp(1 << 40, 1, 1 << 31, *hp, step, None, None, None) == NUMEL
+    assert lib.mamw_adamw_mt_step(1 << 40, 1, 1 << 31, 3e-4, 0.1, 0.05, 0.9, 0.95, 0.1, 1e-8, None) == NUMEL

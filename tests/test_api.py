@@ -189,19 +189,21 @@ def test_pytorch_wrapper_matches_oracle_on_cpu():
 
 
 def test_adamw_step_counter_host_and_device_views():
-    """step_num is a host int until a gradient-scaler step moves the counter to
-    the device; reading it then reads the device counter back, and assigning it
-    (e.g. load_state_dict) returns it to the host."""
+    """step_num is a host int until a gradient-scaler (or capturable) step moves
+    the counter to the device; reading it then reads the device counter back,
+    and assigning it (e.g. load_state_dict) fills that same counter tensor in
+    place, so a step captured in a graph keeps advancing the live counter."""
     from triton_muon_adamw.adamw import HipAdamW
 
     opt = HipAdamW([nn.Parameter(torch.zeros(4))])
     assert opt.step_num == 0 and opt._dev_steps == {}
     opt.step_num = 7
     assert opt.step_num == 7
-    opt._dev_steps = {torch.device("cpu"): torch.tensor(9.0)}  # as _step_amp leaves it
+    counter = torch.tensor(9.0)
+    opt._dev_steps = {torch.device("cpu"): counter}  # as _step_amp leaves it
     assert opt.step_num == 9
     opt.step_num = 3
-    assert opt.step_num == 3 and opt._dev_steps == {}
+    assert opt.step_num == 3 and opt._dev_steps[torch.device("cpu")] is counter and counter.item() == 3.0
     assert MuonAdamW._step_supports_amp_scaling
 
 

@@ -375,3 +375,52 @@ def test_capture_refuses_a_plan_change(gpu):
     opt.step()  # eager steps still work after the failed capture
     torch.cuda.synchronize()
     assert opt.adamw.step_num == 1
+
+
+def test_load_state_dict_keeps_the_captured_step_counter(gpu):
+    """``capturable=True``: loading a checkpoint after a step was captured
+    writes the loaded step into the device counter the graph advances (the
+    tensor is kept, not replaced), so replays after the load follow the loaded
+    step: bit for bit equal to an eager twin loaded from the same checkpoint,
+    and ``step_num`` reads the loaded step plus the replays."""
+    a, b = _params(gpu), _params(gpu)
+    opt_a = MuonAdamW(_split(a), muon_config=MC, adam_config=AC, parameter_split="explicit", capturable=True)
+    opt_b = MuonAdamW(_split(b), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    opt_a.muon.concurrent_flops_limit = opt_b.muon.concurrent_flops_limit = 0.0
+    gen = torch.Generator(device=gpu).manual_seed(21)
+    grads = _grads(a, gpu, gen)
+    _set(a, grads)
+    _set(b, grads)
+    opt_a.step()
+    opt_b.step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        opt_a.step()
+
+    def replay_both(grads):
+        for (_, p, _), g in zip(a, grads):
+            p.grad.copy_(g)
+        graph.replay()
+        _set(b, grads)
+        opt_b.step()
+        torch.cuda.synchronize()
+
+    replay_both(_grads(a, gpu, gen))  # step 2 on both
+    saved = copy.deepcopy(opt_b.state_dict())
+    saved_params = [p.detach().clone() for _, p, _ in b]
+    for _ in range(2):  # steps 3 and 4
+        replay_both(_grads(a, gpu, gen))
+    assert opt_a.adamw.step_num == 4
+    with torch.no_grad():
+        for named in (a, b):
+            for (_, p, _), s in zip(named, saved_params):
+                p.copy_(s)
+    opt_a.load_state_dict(copy.deepcopy(saved))
+    opt_b.load_state_dict(copy.deepcopy(saved))
+    assert opt_a.adamw.step_num == 2
+    for k in range(2):  # steps 3 and 4 again, from the checkpoint
+        replay_both(_grads(a, gpu, gen))
+        for (n, p, _), (_, q, _) in zip(a, b):
+            assert torch.equal(p, q), (k, n)
+    assert opt_a.adamw.step_num == 4 and opt_b.adamw.step_num == 4

@@ -286,14 +286,22 @@ __global__ __launch_bounds__(64) void adamw_bias_kernel(const float* __restrict_
     }
 }
 
-int adamw_mt_launch(const void* device_table, int n_tensors, int64_t n_blocks, const AdamWConsts& c,
-                    mamw_stream_t stream) {
+// Host validation shared by both multi-tensor entry points, complete before
+// any HIP call: MAMW_OK with *launch = false when there is nothing to do.
+int adamw_mt_validate(const void* device_table, int n_tensors, int64_t n_blocks, bool* launch) {
+    *launch = false;
     if (n_tensors < 0 || n_tensors > kMaxTensors) return MAMW_ERR_COUNT;
     if (n_blocks < 0 || n_blocks > int64_t(0x7fffffff)) return MAMW_ERR_NUMEL;
     if (n_blocks == 0) return MAMW_OK;
     if (n_tensors == 0) return MAMW_ERR_COUNT;
     if (!device_table) return MAMW_ERR_NULL;
     if (reinterpret_cast<uintptr_t>(device_table) % 16) return MAMW_ERR_ALIGN;
+    *launch = true;
+    return MAMW_OK;
+}
+
+int adamw_mt_launch(const void* device_table, int n_tensors, int64_t n_blocks, const AdamWConsts& c,
+                    mamw_stream_t stream) {
     // Algorithmic bytes (28 per element) are not known here: the table is in device memory.
     return int(launch(K_ADAMW_MT, 0, 0.0, 0.0, adamw_mt_kernel, dim3(unsigned(n_blocks)), dim3(kAdamWThreads),
                       static_cast<hipStream_t>(stream), static_cast<const AdamWRec*>(device_table), n_tensors, c));
@@ -303,24 +311,25 @@ int adamw_mt_launch(const void* device_table, int n_tensors, int64_t n_blocks, c
 extern "C" int mamw_adamw_mt_step(const void* device_table, int n_tensors, int64_t n_blocks,
                                   float lr, float bias1, float bias2, float beta1, float beta2,
                                   float weight_decay, float eps, mamw_stream_t stream) {
+    bool go = false;
+    const int st = adamw_mt_validate(device_table, n_tensors, n_blocks, &go);
+    if (st != MAMW_OK || !go) return st;
     AdamWScalars s{lr, bias1, bias2, beta1, beta2, weight_decay, eps};
     return adamw_mt_launch(device_table, n_tensors, n_blocks, make_consts(s), stream);
 }
 
-extern "C" int mamw_adamw_mt_step_amp(const void* device_table, int n_tensors, int64_t n_blocks,
+extern "C" int mamw_adamw_mt_step_amp(void* device_table, int n_tensors, int64_t n_blocks,
                                       float lr, double beta1, double beta2, float weight_decay, float eps,
                                       const float* step, const float* grad_scale, const float* found_inf,
                                       mamw_stream_t stream) {
     if (!step) return MAMW_ERR_NULL;
-    if (n_tensors < 0 || n_tensors > kMaxTensors) return MAMW_ERR_COUNT;
-    if (n_blocks <= 0) return n_blocks < 0 ? MAMW_ERR_NUMEL : MAMW_OK;
-    if (n_tensors == 0) return MAMW_ERR_COUNT;
-    if (!device_table) return MAMW_ERR_NULL;
-    if (reinterpret_cast<uintptr_t>(device_table) % 16) return MAMW_ERR_ALIGN;
+    bool go = false;
+    const int vs = adamw_mt_validate(device_table, n_tensors, n_blocks, &go);
+    if (vs != MAMW_OK || !go) return vs;
     AdamWScalars s{lr, 1.0f, 1.0f, float(beta1), float(beta2), weight_decay, eps};
     AdamWConsts c = make_consts(s);
     // The table's trailing record (after n_tensors records) holds the two corrections.
-    float* bias = reinterpret_cast<float*>(static_cast<AdamWRec*>(const_cast<void*>(device_table)) + n_tensors);
+    float* bias = reinterpret_cast<float*>(static_cast<AdamWRec*>(device_table) + n_tensors);
     c.bias = bias;
     c.grad_scale = grad_scale;
     c.found_inf = found_inf;

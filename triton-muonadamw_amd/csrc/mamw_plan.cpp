@@ -9,13 +9,14 @@ namespace {
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-// Byte ranges [a, a+na) and [b, b+nb) overlap.
-bool overlap(const void* a, size_t na, const void* b, size_t nb) {
+bool overlap(const void* a, size_t na, const void* b, size_t nb) { return ranges_overlap(a, na, b, nb); }
+
+}  // namespace
+
+bool ranges_overlap(const void* a, size_t na, const void* b, size_t nb) {
     uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
     return na && nb && pa < pb + nb && pb < pa + na;
 }
-
-}  // namespace
 
 // ---------------------------------------------------------------------------
 // AdamW

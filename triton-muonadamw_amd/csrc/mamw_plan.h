@@ -100,6 +100,9 @@ constexpr int64_t kMaxMatElems = int64_t(1) << 34;   // padded m*n per matrix
 constexpr int64_t kMaxNumel = int64_t(1) << 40;      // AdamW elements per tensor
 constexpr int kMaxTensors = 1 << 20;
 
+// Byte ranges [a, a+na) and [b, b+nb) overlap (empty ranges never do).
+bool ranges_overlap(const void* a, size_t na, const void* b, size_t nb);
+
 inline int64_t round_up(int64_t x, int64_t to) { return (x + to - 1) / to * to; }
 inline size_t align_ws(size_t x) { return (x + kWsAlign - 1) / kWsAlign * kWsAlign; }
 

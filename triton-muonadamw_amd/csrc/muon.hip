@@ -1145,6 +1145,7 @@ int check_ns_dims(int batch, int64_t m, int64_t k) {
     return MAMW_OK;
 }
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+size_t bf16_bytes(int batch, int64_t r, int64_t c) { return size_t(batch) * size_t(r) * size_t(c) * 2; }
 }  // namespace
 
 extern "C" int mamw_ns_gram(const uint16_t* X, uint16_t* A, int batch, int64_t m, int64_t k,
@@ -1153,6 +1154,7 @@ extern "C" int mamw_ns_gram(const uint16_t* X, uint16_t* A, int batch, int64_t m
     if (st != MAMW_OK) return st;
     if (!X || !A) return MAMW_ERR_NULL;
     if (!al16(X) || !al16(A)) return MAMW_ERR_ALIGN;
+    if (ranges_overlap(X, bf16_bytes(batch, m, k), A, bf16_bytes(batch, m, m))) return MAMW_ERR_ALIAS;
     const int tile = (m % 256 == 0) ? choose_tile(m, batch) : 128;
     MuonBatchDescs d{};
     return int(launch_gemm<MODE_GRAM>(tile, gram_args(X, A, m, k, tile), d, batch,
@@ -1166,7 +1168,7 @@ extern "C" int mamw_ns_poly(const uint16_t* A, uint16_t* B, int batch, int64_t m
     if (st != MAMW_OK) return st;
     if (!A || !B) return MAMW_ERR_NULL;
     if (!al16(A) || !al16(B)) return MAMW_ERR_ALIGN;
-    if (A == B) return MAMW_ERR_ALIAS;
+    if (ranges_overlap(A, bf16_bytes(batch, m, m), B, bf16_bytes(batch, m, m))) return MAMW_ERR_ALIAS;
     const int tile = (m % 256 == 0) ? choose_tile(m, batch) : 128;
     MuonBatchDescs d{};
     return int(launch_gemm<MODE_POLY>(tile, poly_args(A, B, m, tile, b, c), d, batch,
@@ -1182,7 +1184,14 @@ extern "C" int mamw_ns_update(const uint16_t* B, const uint16_t* X, const uint16
     if (n % 128) return MAMW_ERR_SHAPE;
     if (!B || !X || !XT || !out) return MAMW_ERR_NULL;
     if (!al16(B) || !al16(X) || !al16(XT) || !al16(out) || (out_t && !al16(out_t))) return MAMW_ERR_ALIGN;
-    if (out_t && (out_t == XT)) return MAMW_ERR_ALIAS;
+    // out is written from B and XT (operands and epilogue source); out_t too, and
+    // from neither orientation of the other output.  out may equal X: X enters
+    // only through XT.
+    const size_t bb = bf16_bytes(batch, m, m), xb = bf16_bytes(batch, m, n);
+    if (ranges_overlap(out, xb, B, bb) || ranges_overlap(out, xb, XT, xb)) return MAMW_ERR_ALIAS;
+    if (out_t && (ranges_overlap(out_t, xb, B, bb) || ranges_overlap(out_t, xb, XT, xb) ||
+                  ranges_overlap(out_t, xb, out, xb)))
+        return MAMW_ERR_ALIAS;
     (void)X;  // X enters through its transpose XT (operand and epilogue source)
     const int tile = (m % 256 == 0 && n % 256 == 0) ? choose_tile(m, batch) : 128;
     MuonBatchDescs d{};
@@ -1196,7 +1205,7 @@ extern "C" int mamw_transpose_bf16(const uint16_t* src, uint16_t* dst, int batch
     if (batch < 1 || batch > 65535) return MAMW_ERR_COUNT;
     if (rows < 1 || cols < 1 || rows > kMaxDim || cols > kMaxDim) return MAMW_ERR_SHAPE;
     if (!src || !dst) return MAMW_ERR_NULL;
-    if (src == dst) return MAMW_ERR_ALIAS;
+    if (ranges_overlap(src, bf16_bytes(batch, rows, cols), dst, bf16_bytes(batch, rows, cols))) return MAMW_ERR_ALIAS;
     const int tr = int((rows + 63) / 64), tc = int((cols + 63) / 64);
     return int(launch(K_TRANSPOSE, 0, 0.0, 4.0 * double(batch) * double(rows) * double(cols), transpose_bf16_kernel,
                       dim3(unsigned(tr * tc), unsigned(batch)), dim3(256), static_cast<hipStream_t>(stream), src, dst,

@@ -12,6 +12,7 @@ from __future__ import annotations
 
 import concurrent.futures as cf
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -43,7 +44,31 @@ COMMON_FLAGS = [
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Per-kernel register / LDS / scratch report, read by scratch_offenders().
+    "-Rpass-analysis=kernel-resource-usage",
 ]
+
+
+def scratch_offenders(remarks: str) -> list[tuple[str, int]]:
+    """Kernels whose resource-usage remark reports private scratch memory.
+
+    Returns ``(mangled kernel name, bytes per lane)`` for every kernel with a
+    non-zero ``ScratchSize``.  No kernel of this library may use scratch: a
+    GEMM whose accumulators or fragments spill runs many times slower (a
+    spilling variant of the Newton-Schulz GEMM once took minutes per launch),
+    so a build that would produce one fails instead.
+    """
+    out: list[tuple[str, int]] = []
+    name = None
+    for line in remarks.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and name is not None and int(m.group(1)) > 0:
+            out.append((name, int(m.group(1))))
+    return out
 
 
 def _hipcc() -> str:
@@ -66,9 +91,17 @@ def _compile(src: Path, obj: Path, verbose: bool) -> None:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")
+    bad = scratch_offenders(res.stderr)
+    if bad:
+        obj.unlink(missing_ok=True)
+        raise RuntimeError(f"{src.name}: kernels use scratch memory (spilled registers or private arrays), "
+                           "which this library does not allow: "
+                           + ", ".join(f"{n} ({b} bytes/lane)" for n, b in bad))
     if verbose and res.stderr.strip():
-        # hipcc's host pass warns that it does not know the packed-fp32 feature.
-        lines = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln]
+        # hipcc's host pass warns that it does not know the packed-fp32 feature;
+        # the resource-usage remarks were checked above.
+        lines = [ln for ln in res.stderr.splitlines()
+                 if "packed-fp32-ops" not in ln and "kernel-resource-usage" not in ln]
         if any(ln.strip() for ln in lines):
             print("\n".join(lines), flush=True)
 

@@ -157,8 +157,18 @@ class HipAdamW:
 
     @step_num.setter
     def step_num(self, value: int) -> None:
+        """Set the counter.  Once device-side counters exist they are filled in
+        place and kept: a step captured in a graph writes to those very
+        tensors, so replacing them would leave the graph advancing freed
+        memory while the bias corrections ignored the new value."""
         self._step_host = int(value)
-        self._dev_steps: dict[torch.device, torch.Tensor] = {}
+        devs = getattr(self, "_dev_steps", None)
+        if devs:
+            with torch.no_grad():
+                for c in devs.values():
+                    c.fill_(float(value))
+        else:
+            self._dev_steps: dict[torch.device, torch.Tensor] = {}
 
     def _refresh_plans(self, active: list[nn.Parameter]) -> None:
         key = tuple((id(p), p.data_ptr(), p.grad.data_ptr(), p.dtype, p.grad.dtype) for p in active)

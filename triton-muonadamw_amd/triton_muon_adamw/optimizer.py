@@ -32,18 +32,14 @@ ParameterGroups: TypeAlias = dict[str, list[nn.Parameter]]
 
 @dataclass
 class AdamConfig:
-    """Hyperparameters for the AdamW branch of :class:`MuonAdamW`.
+    """Settings of the elementwise branch (every parameter that is not a
+    Muon matrix).
 
-    Parameters
-    ----------
-    lr:
-        Learning rate used by AdamW.
-    betas:
-        Coefficients of the first- and second-moment running averages.
-    eps:
-        Term added to the denominator for numerical stability.
-    weight_decay:
-        Decoupled AdamW weight decay coefficient.
+    ``lr`` is the AdamW step size.  ``betas`` = (decay of the gradient mean,
+    decay of the squared-gradient mean).  ``eps`` is added to
+    ``sqrt(v_hat)`` before the division, so a tensor whose second moment is
+    still zero gets a finite step.  ``weight_decay`` shrinks the parameter by
+    ``lr * weight_decay`` each step, outside the adaptive term.
     """
 
     lr: float = 1e-3
@@ -54,26 +50,17 @@ class AdamConfig:
 
 @dataclass
 class MuonConfig:
-    """Hyperparameters for the Muon branch of :class:`MuonAdamW`.
+    """Settings of the matrix branch (orthogonalised momentum updates).
 
-    Parameters
-    ----------
-    lr:
-        Learning rate used by Muon.
-    beta:
-        Momentum coefficient.
-    eps:
-        Lower clamp of the Frobenius norm used to normalise the update.
-    weight_decay:
-        Decoupled weight decay coefficient (applied with the unscaled ``lr``).
-    coeffs:
-        Coefficients (a, b, c) of the Newton-Schulz polynomial.
-    nesterov:
-        Whether to use Nesterov momentum.
-    ns_steps:
-        Number of Newton-Schulz iterations.
-    adjust_lr_fn:
-        Learning-rate scaling by matrix shape.
+    ``lr`` is the base step size; ``adjust_lr_fn`` picks how it is rescaled by
+    the matrix shape (``"original"``: ``sqrt(max(1, rows/cols))``,
+    ``"match_rms_adamw"``: ``0.2 * sqrt(max(rows, cols))``,
+    ``"spectral_unclamped"``: ``sqrt(rows/cols)``).  ``beta`` is the momentum
+    decay and ``nesterov`` selects the look-ahead blend of gradient and
+    momentum.  ``eps`` floors the Frobenius norm the momentum is divided by
+    before the iteration.  ``weight_decay`` multiplies the unscaled ``lr``.
+    ``coeffs`` = (a, b, c) of the quintic ``aX + b(XX^T)X + c(XX^T)^2 X`` that
+    is applied ``ns_steps`` times.
     """
 
     lr: float = 1e-3
@@ -343,7 +330,7 @@ class PyTorchMuonAdamW:
         )
 
     def step(self, closure=None):
-        """Apply one reference AdamW and Muon update (``closure`` as torch.optim)."""
+        """torch's AdamW step, then torch's Muon step (``closure`` as torch.optim)."""
         loss = None
         if closure is not None:
             with torch.enable_grad():
@@ -353,19 +340,19 @@ class PyTorchMuonAdamW:
         return loss
 
     def zero_grad(self, *args, **kwargs) -> None:
-        """Reset gradients for both reference optimizers (torch's default: to None)."""
+        """Clear the gradients of both torch optimizers (torch's default: set to None)."""
         self.adamw.zero_grad(*args, **kwargs)
         self.muon.zero_grad(*args, **kwargs)
 
     def state_dict(self) -> dict[str, object]:
-        """The serialized state of both torch optimizers."""
+        """``{"adam": torch AdamW state, "muon": torch Muon state}``."""
         return {
             "adam": self.adamw.state_dict(),
             "muon": self.muon.state_dict(),
         }
 
     def load_state_dict(self, state_dict: dict[str, object]) -> None:
-        """Load a state dictionary produced by :meth:`state_dict`."""
+        """Hand each branch's entry of a :meth:`state_dict` result to its torch optimizer."""
         if "adam" in state_dict:
             self.adamw.load_state_dict(state_dict["adam"])
         if "muon" in state_dict:
