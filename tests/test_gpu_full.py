@@ -7,10 +7,13 @@ reference named by the reference repo (muon_adamw_benchmark.py:60-66,130-134).
   parameters within 1e-6, each Muon update within bf16 noise (relative
   Frobenius error <= 1e-2).
 * One Llama-3-8B decoder layer plus 1/32 of the AdamW set, same checks.
-* The full Llama-3-8B-shaped step (config 5) through size-independent
-  properties: finite results; AdamW bit-exact per element against the oracle
-  on sampled rows; every Muon update's mean squared singular value inside the
-  band the quintic maps [3e-3, 1] to.
+* The full Llama-3-8B-shaped step (config 5): finite results; AdamW
+  bit-exact per element against the oracle on sampled rows; and, for the
+  first and the last matrix of each of the step's nine launch groups (groups
+  of 16-32 matrices at full size: the launches the headline runs), the
+  orthogonalised update against torch's own Newton-Schulz
+  (``torch.optim._muon._zeropower_via_newtonschulz``) of the same Nesterov
+  blend on the GPU, relative Frobenius error <= 1e-2.
 """
 
 import math
@@ -93,11 +96,22 @@ def test_llama8b_full_step_properties(gpu):
         p = torch.nn.Parameter(torch.empty(shape, device=gpu).normal_(0.0, 0.02, generator=gen))
         p.grad = torch.empty(shape, device=gpu).normal_(0.0, 1e-3, generator=gen)
         named.append((name, p, branch))
-    muon_keep = {n: p.detach().clone() for n, p, b in named if b == "muon" and n.startswith(("l0.", "l31."))}
     rows = torch.arange(0, 128256, 997, device=gpu)
     adam_keep = {n: (p.detach()[rows].cpu().numpy(), p.grad[rows].cpu().numpy())
                  for n, p, b in named if n in ("embed", "lm_head")}
     opt = MuonAdamW(_split(named), muon_config=MC, adam_config=AC, parameter_split="explicit")
+    # The launch groups the step will run (built now, as step() builds them).
+    muon_params = [p for _, p, b in named if b == "muon"]
+    opt.muon._build_calls(muon_params)
+    by_ptr = {p.data_ptr(): (n, p) for n, p, b in named if b == "muon"}
+    picked = {}
+    for call in opt.muon._calls:
+        for i in (0, call.n - 1):
+            n, p = by_ptr[call.arr[i].param]
+            picked[n] = p
+    assert len(opt.muon._calls) == 9 and max(c.n for c in opt.muon._calls) >= 20
+    assert len(picked) == 18
+    muon_keep = {n: p.detach().clone() for n, p in picked.items()}
     opt.step()
     torch.cuda.synchronize()
     for n, p, b in named:
@@ -109,10 +123,17 @@ def test_llama8b_full_step_properties(gpu):
                                               bias2=b2, beta1=0.9, beta2=0.95, weight_decay=0.1, eps=1e-8)
         assert np.array_equal(p.detach()[rows].cpu().numpy(), exp), n
     keep = 1 - MC.lr * MC.weight_decay
-    params = dict((nn_, pp) for nn_, pp, _ in named)
     for n, p0 in muon_keep.items():
-        p = params[n]
+        p = picked[n]
         adj = MC.lr * math.sqrt(max(1.0, p.shape[0] / p.shape[1]))
         u = (p0.double() * keep - p.detach().double()) / adj
         mean_sq = (u.norm() ** 2 / min(p.shape)).item()  # mean of sigma_i^2 of the update
         assert 0.68**2 < mean_sq < 1.21**2, f"{n}: mean squared singular value {mean_sq}"
+        # torch's Newton-Schulz on the same blend (zero momentum before the step)
+        g = p.grad
+        mom = torch.zeros_like(g).lerp_(g, 1 - MC.beta)
+        blend = g.lerp(mom, MC.beta)
+        ref = torch.optim._muon._zeropower_via_newtonschulz(blend, MC.coeffs, MC.ns_steps, MC.eps)
+        err = ((u - ref.double()).norm() / ref.double().norm()).item()
+        assert err <= 1e-2, f"{n}: update rel err {err} against torch's Newton-Schulz"
+        del u, ref, mom, blend

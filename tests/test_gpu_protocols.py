@@ -1,0 +1,225 @@
+"""GPU parity under the reference's own protocols and its non-default options.
+
+* Long horizon (muon_adamw_benchmark.py:99-134): the reference steps its
+  hybrid optimizer and the torch wrapper many times on static gradients and
+  then compares every parameter at atol = rtol = 1e-2.  Here: the
+  GPT-2-124M-shaped set (config 4), 150 static-gradient steps (one 50 + 100
+  loop of that script), this build against ``PyTorchMuonAdamW`` on the GPU.
+* ``parameter_split="auto"`` (optimizer.py:117-130, the reference's default)
+  on an HF-style module: ``get_input_embeddings`` / ``get_output_embeddings``,
+  a head tied to the embedding (deduplicated by ``data_ptr``), a frozen
+  weight (skipped), a 2-D position embedding that goes to Muon; real
+  backward passes; three steps against ``PyTorchMuonAdamW(..., "auto")``.
+* ``adjust_lr_fn`` (triton_muon.py:424-431): ``"match_rms_adamw"`` against
+  ``torch.optim.Muon`` with the same option; ``"spectral_unclamped"`` (which
+  torch does not have) against the CPU oracle.
+"""
+
+import copy
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+import oracle
+from helpers import gpt2_layout, rel_fro
+from triton_muon_adamw import AdamConfig, MuonAdamW, MuonConfig, PyTorchMuonAdamW
+from triton_muon_adamw.muon import HipMuon
+
+pytestmark = pytest.mark.gpu
+
+COEFFS = (3.4445, -4.7750, 2.0315)
+AC = AdamConfig(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+
+
+def _mc(**kw):
+    base = dict(lr=1e-3, beta=0.95, eps=1e-7, weight_decay=0.1, coeffs=COEFFS, nesterov=True, ns_steps=5)
+    base.update(kw)
+    return MuonConfig(**base)
+
+
+def _split(named):
+    return {"adam": [p for _, p, b in named if b == "adam"], "muon": [p for _, p, b in named if b == "muon"]}
+
+
+def test_gpt2_long_horizon_static_gradients(gpu):
+    """150 steps on one fixed set of gradients, then every parameter within
+    atol = rtol = 1e-2 of the torch wrapper's (the reference's end check,
+    muon_adamw_benchmark.py:128-134), AdamW parameters within 1e-5."""
+    mc = _mc()
+    gen = torch.Generator(device=gpu).manual_seed(3)
+    mine, theirs = [], []
+    for name, shape, branch in gpt2_layout():
+        w = torch.empty(shape, device=gpu).normal_(0.0, 0.02, generator=gen)
+        g = torch.empty(shape, device=gpu).normal_(0.0, 1e-3, generator=gen)
+        p, q = nn.Parameter(w.clone()), nn.Parameter(w.clone())
+        p.grad, q.grad = g.clone(), g.clone()
+        mine.append((name, p, branch))
+        theirs.append((name, q, branch))
+    start = [p.detach().clone() for _, p, _ in mine]
+    opt = MuonAdamW(_split(mine), muon_config=mc, adam_config=AC, parameter_split="explicit")
+    ref = PyTorchMuonAdamW(_split(theirs), muon_config=mc, adam_config=AC, parameter_split="explicit")
+    for _ in range(150):
+        opt.step()
+        ref.step()
+    torch.cuda.synchronize()
+    for (name, p, b), (_, q, _), p0 in zip(mine, theirs, start):
+        assert torch.isfinite(p).all(), name
+        torch.testing.assert_close(p.detach(), q.detach(), atol=1e-2, rtol=1e-2, msg=name)
+        if b == "adam":
+            torch.testing.assert_close(p.detach(), q.detach(), atol=1e-5, rtol=0, msg=name)
+        else:
+            # not vacuous: each matrix moved (relative Frobenius) at least 20x more
+            # than it differs from the torch wrapper's
+            moved = ((p.detach() - p0).norm() / p0.norm()).item()
+            diff = ((p.detach() - q.detach()).norm() / p0.norm()).item()
+            assert moved > 20 * diff, (name, moved, diff)
+
+
+class _TinyLM(nn.Module):
+    """A GPT-style module with the HF accessors ``auto`` routing uses."""
+
+    def __init__(self, vocab=1000, d=256, n_ctx=128, n_layer=2):
+        super().__init__()
+        self.wte = nn.Embedding(vocab, d)
+        self.wpe = nn.Embedding(n_ctx, d)
+        self.blocks = nn.ModuleList()
+        for _ in range(n_layer):
+            self.blocks.append(nn.ModuleDict({
+                "ln": nn.LayerNorm(d), "fc": nn.Linear(d, 4 * d), "proj": nn.Linear(4 * d, d),
+                "attn": nn.Linear(d, 3 * d), "out": nn.Linear(d, d)}))
+        self.frozen = nn.Linear(d, d)
+        self.frozen.weight.requires_grad_(False)
+        self.ln_f = nn.LayerNorm(d)
+        self.lm_head = nn.Linear(d, vocab, bias=False)
+        self.lm_head.weight = self.wte.weight  # tied
+
+    def get_input_embeddings(self):
+        return self.wte
+
+    def get_output_embeddings(self):
+        return self.lm_head
+
+    def forward(self, idx):
+        pos = torch.arange(idx.shape[1], device=idx.device)
+        h = self.wte(idx) + self.wpe(pos)[None]
+        for blk in self.blocks:
+            a = blk["attn"](blk["ln"](h))
+            h = h + blk["out"](a[..., : h.shape[-1]] * torch.sigmoid(a[..., h.shape[-1]:2 * h.shape[-1]]))
+            h = h + blk["proj"](torch.relu(blk["fc"](h)))
+        h = h + self.frozen(h)
+        return self.lm_head(self.ln_f(h))
+
+
+def test_auto_split_on_an_hf_style_module(gpu):
+    torch.manual_seed(0)
+    model_a = _TinyLM().to(gpu)
+    model_b = copy.deepcopy(model_a)
+    mc = _mc(lr=2e-2)
+    opt = MuonAdamW(model_a, muon_config=mc, adam_config=AC, parameter_split="auto")
+    ref = PyTorchMuonAdamW(model_b, muon_config=mc, adam_config=AC, parameter_split="auto")
+    names_a = {id(p): n for n, p in model_a.named_parameters()}
+    muon_names = [names_a[id(p)] for p in opt.param_group["muon"]]
+    adam_names = [names_a[id(p)] for p in opt.param_group["adam"]]
+    # the reference's rules (optimizer.py:117-130): wpe is 2-D and not the input embedding -> Muon;
+    # the tied head is the embedding's storage -> seen once, as the embedding; the frozen weight is skipped
+    assert "wpe.weight" in muon_names and "wte.weight" in adam_names
+    assert "frozen.weight" not in muon_names + adam_names and "frozen.bias" in adam_names
+    assert len(muon_names + adam_names) == len(set(muon_names + adam_names))
+    names_b = {id(p): n for n, p in model_b.named_parameters()}
+    assert [names_b[id(p)] for p in ref.muon.param_groups[0]["params"]] == muon_names
+    assert [names_b[id(p)] for p in ref.adamw.param_groups[0]["params"]] == adam_names
+
+    gen = torch.Generator(device=gpu).manual_seed(1)
+    keep = 1 - mc.lr * mc.weight_decay
+    for _ in range(3):
+        idx = torch.randint(0, 1000, (4, 64), device=gpu, generator=gen)
+        tgt = torch.randint(0, 1000, (4, 64), device=gpu, generator=gen)
+        for m, o in ((model_a, opt), (model_b, ref)):
+            o.zero_grad()
+            loss = nn.functional.cross_entropy(m(idx).flatten(0, 1), tgt.flatten())
+            loss.backward()
+        before = {n: p.detach().clone() for n, p in model_b.named_parameters()}
+        opt.step()
+        ref.step()
+        torch.cuda.synchronize()
+        pb = dict(model_b.named_parameters())
+        for n, p in model_a.named_parameters():
+            q = pb[n]
+            torch.testing.assert_close(p.detach(), q.detach(), atol=1e-2, rtol=1e-2, msg=n)
+            if n in adam_names or n == "lm_head.weight":
+                torch.testing.assert_close(p.detach(), q.detach(), atol=1e-6, rtol=0, msg=n)
+            elif n in muon_names:
+                adj = mc.lr * math.sqrt(max(1.0, p.shape[0] / p.shape[1]))
+                u_mine = (before[n].double() * keep - p.detach().double()) / adj
+                u_ref = (before[n].double() * keep - q.detach().double()) / adj
+                err = ((u_mine - u_ref).norm() / u_ref.norm()).item()
+                assert err <= 1e-2, f"{n}: update rel err {err}"
+            else:  # frozen weight: untouched by both
+                assert n == "frozen.weight" and torch.equal(p, before[n])
+        # both sides keep the model's parameters synchronised for the next step
+        with torch.no_grad():
+            for n, p in model_a.named_parameters():
+                p.copy_(pb[n])
+
+
+SHAPES = [(256, 768), (768, 256), (384, 384), (1024, 300)]
+
+
+@pytest.mark.parametrize("adjust", ["match_rms_adamw", "original"])
+def test_adjust_lr_fn_against_torch_muon(gpu, adjust):
+    """Two steps of HipMuon and torch.optim.Muon (same adjust_lr_fn) on the
+    same parameters and gradients: updates within 1e-2 relative Frobenius,
+    parameters within the reference tolerance."""
+    gen = torch.Generator(device=gpu).manual_seed(7)
+    ps = [torch.empty(s, device=gpu).normal_(0.0, 0.02, generator=gen) for s in SHAPES]
+    mine = [nn.Parameter(p.clone()) for p in ps]
+    theirs = [nn.Parameter(p.clone()) for p in ps]
+    opt = HipMuon(mine, lr=2e-2, weight_decay=0.1, coeffs=COEFFS, nesterov=True, beta=0.95, ns_steps=5, eps=1e-7,
+                  adjust_lr_fn=adjust)
+    ref = torch.optim.Muon(theirs, lr=2e-2, weight_decay=0.1, momentum=0.95, nesterov=True, ns_coefficients=COEFFS,
+                           eps=1e-7, ns_steps=5, adjust_lr_fn=adjust)
+    keep = 1 - 2e-2 * 0.1
+    for _ in range(2):
+        for p, q in zip(mine, theirs):
+            g = torch.empty(p.shape, device=gpu).normal_(0.0, 1.0, generator=gen)
+            p.grad, q.grad = g.clone(), g.clone()
+        before = [q.detach().clone() for q in theirs]
+        opt.step()
+        ref.step()
+        torch.cuda.synchronize()
+        for p, q, b0 in zip(mine, theirs, before):
+            adj = torch.optim._muon._adjust_lr(2e-2, adjust, p.shape)
+            u_mine = (b0.double() * keep - p.detach().double()) / adj
+            u_ref = (b0.double() * keep - q.detach().double()) / adj
+            assert ((u_mine - u_ref).norm() / u_ref.norm()).item() <= 1e-2, p.shape
+            torch.testing.assert_close(p.detach(), q.detach(), atol=1e-2, rtol=1e-2)
+
+
+def test_adjust_lr_spectral_unclamped_against_oracle(gpu):
+    """``spectral_unclamped`` (reference only, triton_muon.py:430-431): the HIP
+    step against the CPU oracle on the same inputs; momentum bit-exact, the
+    update within 1e-2 relative Frobenius, parameters within 1e-5."""
+    gen = torch.Generator().manual_seed(9)
+    ps = [torch.randn(s, generator=gen) * 0.02 for s in SHAPES]
+    gs = [torch.randn(s, generator=gen) for s in SHAPES]
+    mine = [nn.Parameter(p.clone().to(gpu)) for p in ps]
+    for p, g in zip(mine, gs):
+        p.grad = g.to(gpu)
+    opt = HipMuon(mine, lr=2e-2, weight_decay=0.1, coeffs=COEFFS, nesterov=True, beta=0.95, ns_steps=5, eps=1e-7,
+                  adjust_lr_fn="spectral_unclamped")
+    opt.step()
+    torch.cuda.synchronize()
+    keep = np.float32(1 - 2e-2 * 0.1)
+    for p, p0, g in zip(mine, ps, gs):
+        exp_p, exp_m, exp_u = oracle.muon.muon_update(p0.numpy(), g.numpy(), np.zeros(p0.shape, np.float32),
+                                                      lr=2e-2, weight_decay=0.1, beta=0.95, nesterov=True,
+                                                      coeffs=COEFFS, ns_steps=5, eps=1e-7,
+                                                      adjust_lr_fn="spectral_unclamped")
+        assert np.array_equal(opt.momentum[p].cpu().numpy(), exp_m)
+        adj = oracle.muon.adjust_lr(2e-2, "spectral_unclamped", p0.shape)
+        got_u = (p0.numpy().astype(np.float64) * keep - p.detach().cpu().numpy()) / adj
+        assert rel_fro(got_u, exp_u) <= 1e-2, p0.shape
+        np.testing.assert_allclose(p.detach().cpu().numpy(), exp_p, atol=1e-5, rtol=0)

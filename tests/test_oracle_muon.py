@@ -124,26 +124,56 @@ def test_adjust_lr_closed_forms():
         om.adjust_lr(lr, "nope", (2, 2))
 
 
+@pytest.mark.parametrize("adjust", ["original", "match_rms_adamw"])
 @pytest.mark.parametrize("shape,nesterov", [((64, 96), True), ((96, 64), True), ((80, 80), False)])
-def test_full_step_vs_torch_optim_muon(shape, nesterov):
+def test_full_step_vs_torch_optim_muon(shape, nesterov, adjust):
     rng = np.random.default_rng(6)
     p0 = (rng.standard_normal(shape) * 0.02).astype(np.float32)
     g = rng.standard_normal(shape).astype(np.float32)
     m0 = (rng.standard_normal(shape) * 1e-3).astype(np.float32)
     tp = torch.nn.Parameter(torch.from_numpy(p0.copy()))
     opt = torch.optim.Muon([tp], lr=0.02, weight_decay=0.1, momentum=0.95, nesterov=nesterov,
-                           ns_coefficients=COEFFS, eps=1e-7, ns_steps=5, adjust_lr_fn="original")
+                           ns_coefficients=COEFFS, eps=1e-7, ns_steps=5, adjust_lr_fn=adjust)
     opt.state[tp]["momentum_buffer"] = torch.from_numpy(m0.copy())
     tp.grad = torch.from_numpy(g.copy())
     opt.step()
     op, om_, _ = om.muon_update(p0, g, m0, lr=0.02, weight_decay=0.1, beta=0.95, nesterov=nesterov,
-                                coeffs=COEFFS, ns_steps=5, eps=1e-7)
+                                coeffs=COEFFS, ns_steps=5, eps=1e-7, adjust_lr_fn=adjust)
     assert np.array_equal(om_, opt.state[tp]["momentum_buffer"].numpy())
-    adj = om.adjust_lr(0.02, "original", shape)
+    adj = om.adjust_lr(0.02, adjust, shape)
+    # torch's own scale for this shape (torch/optim/_muon.py:73-84) is the oracle's
+    assert adj == torch.optim._muon._adjust_lr(0.02, adjust, torch.Size(shape))
     # parameter differences are adj * (bf16 noise of the update)
     np.testing.assert_allclose(op, tp.detach().numpy(), rtol=0, atol=adj * 8e-3)
     upd_t = (p0 * np.float32(1 - 0.02 * 0.1) - tp.detach().numpy()) / adj
     upd_o = (p0 * np.float32(1 - 0.02 * 0.1) - op) / adj
+    assert np.linalg.norm(upd_o - upd_t) / np.linalg.norm(upd_t) < 1e-2
+
+
+@pytest.mark.parametrize("shape", [(64, 96), (96, 64)])
+def test_spectral_unclamped_step_vs_torch_direction(shape):
+    """``spectral_unclamped`` exists only in the reference (triton_muon.py:430-431):
+    torch pins the update direction (its "original" step on the same inputs,
+    divided by its own scale) and the reference's closed form sqrt(R/C) the
+    scale; for a tall matrix the two scales coincide."""
+    rng = np.random.default_rng(16)
+    p0 = (rng.standard_normal(shape) * 0.02).astype(np.float32)
+    g = rng.standard_normal(shape).astype(np.float32)
+    tp = torch.nn.Parameter(torch.from_numpy(p0.copy()))
+    opt = torch.optim.Muon([tp], lr=0.02, weight_decay=0.1, momentum=0.95, nesterov=True,
+                           ns_coefficients=COEFFS, eps=1e-7, ns_steps=5, adjust_lr_fn="original")
+    tp.grad = torch.from_numpy(g.copy())
+    opt.step()
+    keep = np.float32(1 - 0.02 * 0.1)
+    adj_t = torch.optim._muon._adjust_lr(0.02, "original", torch.Size(shape))
+    upd_t = (p0 * keep - tp.detach().numpy()) / adj_t
+    op, _, _ = om.muon_update(p0, g, np.zeros_like(p0), lr=0.02, weight_decay=0.1, beta=0.95, nesterov=True,
+                              coeffs=COEFFS, ns_steps=5, eps=1e-7, adjust_lr_fn="spectral_unclamped")
+    adj_o = om.adjust_lr(0.02, "spectral_unclamped", shape)
+    assert adj_o == pytest.approx(0.02 * math.sqrt(shape[0] / shape[1]), rel=1e-15)
+    if shape[0] > shape[1]:
+        assert adj_o == pytest.approx(adj_t, rel=1e-15)
+    upd_o = (p0 * keep - op) / adj_o
     assert np.linalg.norm(upd_o - upd_t) / np.linalg.norm(upd_t) < 1e-2
 
 
