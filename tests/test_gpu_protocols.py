@@ -201,7 +201,8 @@ def test_adjust_lr_fn_against_torch_muon(gpu, adjust):
 def test_adjust_lr_spectral_unclamped_against_oracle(gpu):
     """``spectral_unclamped`` (reference only, triton_muon.py:430-431): the HIP
     step against the CPU oracle on the same inputs; momentum bit-exact, the
-    update within 1e-2 relative Frobenius, parameters within 1e-5."""
+    update within 1e-2 relative Frobenius, parameters within the scale's
+    multiple of 8e-3 (bf16 noise of the update times the step size)."""
     gen = torch.Generator().manual_seed(9)
     ps = [torch.randn(s, generator=gen) * 0.02 for s in SHAPES]
     gs = [torch.randn(s, generator=gen) for s in SHAPES]
@@ -222,4 +223,5 @@ def test_adjust_lr_spectral_unclamped_against_oracle(gpu):
         adj = oracle.muon.adjust_lr(2e-2, "spectral_unclamped", p0.shape)
         got_u = (p0.numpy().astype(np.float64) * keep - p.detach().cpu().numpy()) / adj
         assert rel_fro(got_u, exp_u) <= 1e-2, p0.shape
-        np.testing.assert_allclose(p.detach().cpu().numpy(), exp_p, atol=1e-5, rtol=0)
+        # parameter differences are adj * (bf16 noise of the update), as in the oracle's own pin
+        np.testing.assert_allclose(p.detach().cpu().numpy(), exp_p, atol=adj * 8e-3, rtol=0)

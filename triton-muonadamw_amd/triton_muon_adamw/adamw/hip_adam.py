@@ -181,7 +181,9 @@ class HipAdamW:
     @torch.no_grad()
     def step(self):
         """Performs one iteration of the AdamW optimizer step."""
-        if self.capturable:
+        if self.capturable or self._dev_steps:
+            # The counter lives on the device (capturable, or after a gradient-
+            # scaler step): keep it there, so that no step reads it back.
             self._step_amp(None, None)
             return
         self.step_num += 1
