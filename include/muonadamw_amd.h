@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MAMW_ABI_VERSION 4
+#define MAMW_ABI_VERSION 5
 
 /* ---- status codes -------------------------------------------------------- */
 #define MAMW_OK             0
@@ -47,6 +47,7 @@ extern "C" {
 #define MAMW_ERR_HYPER     -7 /* hyper-parameter out of range (ns_steps, ...)        */
 #define MAMW_ERR_TABLE     -8 /* host table buffer too small                         */
 #define MAMW_ERR_ALIAS     -9 /* buffers that must be distinct overlap               */
+#define MAMW_ERR_SCRATCH  -10 /* step needs more than MAMW_NOALLOC_SCRATCH_BYTES     */
 
 /* A hipStream_t.  NULL selects the null stream. */
 typedef void* mamw_stream_t;
@@ -192,6 +193,31 @@ int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr,
                    double weight_decay, double beta, int nesterov, float a,
                    float b, float c, int ns_steps, float eps, void* workspace,
                    size_t workspace_bytes, mamw_stream_t stream);
+
+/* mamw_muon_step without a caller workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  No counterpart in the reference (its
+ * launchers allocate scratch from torch per call, triton_muon.py:320-321,
+ * 358-359,422).  The workspace is a file-scope device array of
+ * MAMW_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held from the
+ * library's load until the process ends; its device address is resolved once
+ * per device on the first call there.  The call allocates nothing (no
+ * hipMalloc/hipFree, and no profiler events even while profiling is on).
+ * Limits and sharing:
+ *   - a batch whose mamw_muon_workspace_bytes exceeds the array is rejected
+ *     with MAMW_ERR_SCRATCH (one 4096 x 14336 matrix needs 400 MiB; what
+ *     fits: 1 of 4096 x 4096, 9 of 1024 x 4096, 16 of 768 x 3072, 20 of
+ *     768 x 2304, 32 of 768 x 768);
+ *   - every call on one GPU uses that GPU's one array, which keeps the last
+ *     call's contents (nothing in it needs to start at zero: each step writes
+ *     every workspace byte it reads first), so calls that overlap in time on
+ *     one GPU race: issue them on one stream, or order them with events.
+ * Arguments, validation and results are those of mamw_muon_step.            */
+#define MAMW_NOALLOC_SCRATCH_BYTES (256u << 20) /* 256 MiB per GPU */
+int mamw_muon_step_noalloc(const mamw_muon_matrix* mats, int batch, double lr,
+                           double weight_decay, double beta, int nesterov,
+                           float a, float b, float c, int ns_steps, float eps,
+                           mamw_stream_t stream);
 
 /* mamw_muon_step for a gradient-scaler step (torch/amp/grad_scaler.py:403-448;
  * the reference has no mixed-precision path): gradients are divided by the

@@ -13,7 +13,7 @@ from triton_muon_adamw import _lib
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "muonadamw_amd.h"
 
-OK, NULL, COUNT, NUMEL, SHAPE, ALIGN, WS, HYPER, TABLE, ALIAS = 0, -1, -2, -3, -4, -5, -6, -7, -8, -9
+OK, NULL, COUNT, NUMEL, SHAPE, ALIGN, WS, HYPER, TABLE, ALIAS, SCRATCH = 0, -1, -2, -3, -4, -5, -6, -7, -8, -9, -10
 
 
 def declared_functions():
@@ -37,8 +37,8 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_strerror():
     lib = _lib.load()
-    assert lib.mamw_abi_version() == 4
-    for code in (OK, NULL, COUNT, NUMEL, SHAPE, ALIGN, WS, HYPER, TABLE, ALIAS):
+    assert lib.mamw_abi_version() == 5
+    for code in (OK, NULL, COUNT, NUMEL, SHAPE, ALIGN, WS, HYPER, TABLE, ALIAS, SCRATCH):
         msg = lib.mamw_strerror(code).decode()
         assert msg and msg != "unknown status"
     assert lib.mamw_strerror(-1234).decode() == "unknown status"
@@ -233,6 +233,34 @@ def test_muon_step_rejects_before_hip():
     arr = _mats([(256, 512)])
     arr[0].update = arr[0].param + 2
     assert _step(arr, 1) == ALIGN
+
+
+def test_muon_step_noalloc_rejects_before_hip():
+    """The no-allocation entry point validates like mamw_muon_step, and a batch
+    whose workspace exceeds the library's static scratch is rejected with
+    MAMW_ERR_SCRATCH, all before any HIP call."""
+    lib = _lib.load()
+
+    def call(arr, n, steps=5):
+        return lib.mamw_muon_step_noalloc(arr, n, 1e-3, 0.1, 0.95, 1, 3.4445, -4.775, 2.0315, steps, 1e-7, None)
+
+    assert call(_mats([(4096, 14336)]), 1) == SCRATCH  # one 4096 x 14336 matrix needs 400 MiB
+    assert call(_mats([(4096, 4096)] * 2), 2) == SCRATCH
+    assert call(_mats([(1024, 4096)] * 10), 10) == SCRATCH
+    assert call(_mats([(256, 512), (512, 300)]), 2) == SHAPE
+    assert call(_mats([(256, 512)]), 0) == COUNT
+    assert call(_mats([(256, 512)]), 1, steps=100) == HYPER
+    arr = _mats([(256, 512)])
+    arr[0].grad = arr[0].param + 4
+    assert call(arr, 1) == ALIAS
+    assert call(None, 1) == NULL
+    assert "scratch" in lib.mamw_strerror(SCRATCH).decode()
+    # the documented fits (both orientations)
+    for shape, k in (((4096, 4096), 1), ((1024, 4096), 9), ((768, 3072), 16), ((3072, 768), 16),
+                     ((768, 2304), 20), ((768, 768), 32)):
+        n = ctypes.c_size_t()
+        assert lib.mamw_muon_workspace_bytes(k, shape[0], shape[1], 5, ctypes.byref(n)) == OK
+        assert n.value <= 256 << 20, (shape, k, n.value)
 
 
 def test_ns_blocks_validation():

@@ -17,6 +17,8 @@ extern "C" const char* mamw_strerror(int status) {
         case MAMW_ERR_HYPER: return "hyper-parameter out of range";
         case MAMW_ERR_TABLE: return "host table buffer too small";
         case MAMW_ERR_ALIAS: return "buffers that must be distinct overlap";
+        case MAMW_ERR_SCRATCH:
+            return "the step needs more workspace than the library's static scratch (MAMW_NOALLOC_SCRATCH_BYTES)";
         default: break;
     }
     if (status > 0) return hipGetErrorString(static_cast<hipError_t>(status));

@@ -31,8 +31,18 @@ enum KernelId : int32_t {
     K_COUNT
 };
 
-// Returns true and two events when profiling is on.
+// Returns true and two events when profiling is on (and not suspended on
+// this thread).
 bool prof_take(hipEvent_t* start, hipEvent_t* stop);
+
+// While one of these lives, launches on this thread take no profiler events
+// (an entry point that must not allocate creates none).
+struct ProfSuspend {
+    ProfSuspend();
+    ~ProfSuspend();
+    ProfSuspend(const ProfSuspend&) = delete;
+    ProfSuspend& operator=(const ProfSuspend&) = delete;
+};
 void prof_push(int32_t kernel, int32_t variant, double flops, double bytes, hipEvent_t start, hipEvent_t stop);
 
 template <typename Kernel, typename... Args>

@@ -15,6 +15,8 @@
 // All GEMMs are C = A_op * B_op^T over operands stored row-major with the
 // reduction index contiguous (X for the Gram, A for A A since A is symmetric,
 // B and XT for B X), so one MFMA tile kernel serves every product.
+#include <mutex>
+
 #include "mamw_device.h"
 #include "mamw_launch.h"
 
@@ -1128,6 +1130,61 @@ extern "C" int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr
                               mamw_stream_t stream) {
     return muon_step_impl(mats, batch, lr, weight_decay, beta, nesterov, a, b, c, ns_steps, eps, workspace,
                           workspace_bytes, nullptr, nullptr, stream);
+}
+
+// ---------------------------------------------------------------------------
+// mamw_muon_step_noalloc: the Muon workspace in a file-scope device array of
+// fixed size instead of caller memory.  Each GPU the library runs on holds its
+// own copy from module load until the process ends; host code reaches it only
+// through the address hipGetSymbolAddress returns on that device (the array's
+// name in host code is a host-side stand-in, not a device address).
+
+static __device__ __align__(256) unsigned char scratch[MAMW_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];  // device address of `scratch` per device; NULL until resolved
+
+// Device address of `scratch` on the current device, resolved on the first
+// call on that device and kept.
+hipError_t scratch_address(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxScratchDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!p) return hipErrorInvalidSymbol;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+}  // namespace
+
+extern "C" int mamw_muon_step_noalloc(const mamw_muon_matrix* mats, int batch, double lr, double weight_decay,
+                                      double beta, int nesterov, float a, float b, float c, int ns_steps,
+                                      float eps, mamw_stream_t stream) {
+    // Host validation first, against a stand-in workspace address that no
+    // caller buffer can overlap (the real array is the library's own), so
+    // every rejection precedes the first HIP call.
+    MuonPlan p;
+    MuonBatchDescs descs;
+    void* const stand_in = reinterpret_cast<void*>(uintptr_t(kWsAlign));
+    int st = muon_validate(mats, batch, ns_steps, stand_in, ~size_t(0) - kWsAlign, &p, &descs);
+    if (st != MAMW_OK) return st;
+    if (p.bytes > size_t(MAMW_NOALLOC_SCRATCH_BYTES)) return MAMW_ERR_SCRATCH;
+    void* ws = nullptr;
+    const hipError_t e = scratch_address(&ws);
+    if (e != hipSuccess) return int(e);
+    // No per-dispatch profiler events here: creating them would allocate.
+    ProfSuspend no_events;
+    return muon_step_impl(mats, batch, lr, weight_decay, beta, nesterov, a, b, c, ns_steps, eps, ws,
+                          size_t(MAMW_NOALLOC_SCRATCH_BYTES), nullptr, nullptr, stream);
 }
 
 extern "C" int mamw_muon_step_amp(const mamw_muon_matrix* mats, int batch, double lr, double weight_decay,

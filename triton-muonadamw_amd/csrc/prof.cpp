@@ -17,6 +17,7 @@ struct Rec {
 
 std::mutex g_mu;
 bool g_on = false;
+thread_local int g_suspended = 0;  // ProfSuspend nesting depth on this thread
 std::vector<Rec> g_recs;
 std::vector<hipEvent_t> g_free;  // events ready for reuse
 
@@ -48,7 +49,11 @@ const char* const kNames[K_COUNT] = {
 
 }  // namespace
 
+ProfSuspend::ProfSuspend() { ++g_suspended; }
+ProfSuspend::~ProfSuspend() { --g_suspended; }
+
 bool prof_take(hipEvent_t* start, hipEvent_t* stop) {
+    if (g_suspended) return false;
     std::lock_guard<std::mutex> lk(g_mu);
     if (!g_on) return false;
     *start = take_event();

@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libmuonadamw_amd.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 MUON_MAX_BATCH = 32
 BF16_PARAM = 0x1  # MAMW_BF16_PARAM
 BF16_GRAD = 0x2   # MAMW_BF16_GRAD
@@ -103,6 +103,11 @@ _PROTOTYPES = {
         c_int,
         [POINTER(MuonMatrix), c_int, c_double, c_double, c_double, c_int, c_float, c_float, c_float,
          c_int, c_float, c_void_p, c_size_t, c_void_p],
+    ),
+    "mamw_muon_step_noalloc": (
+        c_int,
+        [POINTER(MuonMatrix), c_int, c_double, c_double, c_double, c_int, c_float, c_float, c_float,
+         c_int, c_float, c_void_p],
     ),
     "mamw_muon_step_amp": (
         c_int,
