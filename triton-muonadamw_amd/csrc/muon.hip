@@ -802,41 +802,96 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         *reinterpret_cast<uint4*>(g.c + bat * g.c_bs + off) = wv;
     };
 
-    // 256-wide k-blocked tiles off the diagonal: combine fragment rows 0-1
-    // (tile rows y in [0, 64) and [128, 192), both wave rows), store those
-    // bands, then combine rows 2-3 while the first stores drain.  The two
-    // halves touch disjoint TT cells.
-    constexpr bool SPLIT = BM == 256 && PANEL;
-    bool split_done = false;
-    if constexpr (SPLIT) {
-        static_assert(F == 4 && NT == 32 && NIT == 32, "band layout of the 256 tile");
-        if (!diag) {
-            auto store_bands = [&](int ph) {
+    // k-blocked outputs (every product but APPLY): each store is a 16-byte
+    // buffer store at a 32-bit byte offset inside one output matrix, the sum of
+    // a per-lane part fixed for the tile (voffset) and a wave-uniform part per
+    // piece (soffset), so no per-store address arithmetic is left; a batch's
+    // LDS reads are all issued before its stores, so the batch waits on the
+    // LDS latency once.  With XP = BN/32 and NXQ = BN/32:
+    //   transposed piece it (x = (it%XP)*32 + tid/8, chunk c = (it/XP)*8 + tid%8):
+    //     (ti*BM/64 + it/XP)*rows_t*128 + (tj*BN + (it%XP)*32)*128 + tid*16
+    //   direct piece it (t = 4*it + wave):
+    //     (tj*BN/64 + (t%NXQ)/2)*rows_x*128 + (ti*BM + (t/NXQ)*16)*128 + ((t%NXQ)&1)*64
+    //     + (lane%16)*128 + (lane/16)*16
+    // Diagonal tiles of the symmetric products take the transposed orientation
+    // only: the block equals its mirror, and the MFMA result is exactly
+    // symmetric (element (i,j) and (j,i) are the same products summed in the
+    // same order), which the symmetry tests check bit for bit.
+    if constexpr (PANEL) {
+        constexpr int XP = BN / 32;
+        const int64_t rows_x = int64_t(g.tiles_m) * BM;
+        uint16_t* const out_tr = SYM ? g.c + bat * g.c_bs : g.ct + bat * g.ct_bs;
+        uint16_t* const out_dir = g.c + bat * g.c_bs;
+        const __amdgpu_buffer_rsrc_t r_tr = make_rsrc(out_tr, (SYM ? g.c_bs : g.ct_bs) * 2);
+        const __amdgpu_buffer_rsrc_t r_dir = make_rsrc(out_dir, g.c_bs * 2);
+        const int vo_tr = tid * 16, vo_dir = (lane & 15) * 128 + (lane >> 4) * 16;
+        const int base_tr = int((int64_t(ti) * (BM / 64) * rows_t + int64_t(tj) * BN) * 128);
+        const int base_dir = int((int64_t(tj) * (BN / 64) * rows_x + int64_t(ti) * BM) * 128);
+        const bool tr_on = has_tr, dir_on = has_dir;
+        auto tr_read = [&](int it) {
+            const int x = (it % XP) * 32 + (tid >> 3), c = (it / XP) * 8 + (tid & 7);
+            return *reinterpret_cast<const uint4*>(TT + x * BM + (((c ^ x ^ (x >> 3)) & (NCH - 1)) << 3));
+        };
+        auto tr_soff = [&](int it) {
+            return __builtin_amdgcn_readfirstlane(base_tr + (it / XP) * int(rows_t) * 128 + (it % XP) * 4096);
+        };
+        auto dir_soff = [&](int it) {
+            const int t = it * 4 + wave;
+            return __builtin_amdgcn_readfirstlane(base_dir + ((t % NXQ) / 2) * int(rows_x) * 128 + (t / NXQ) * 2048 +
+                                                  ((t % NXQ) & 1) * 64);
+        };
+        // Pieces it0 .. it0+NB-1 of both orientations.
+        constexpr int NB = 8;
+        typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+        auto vec = [](uint4 w) { return u32x4_t{w.x, w.y, w.z, w.w}; };
+        auto store_batch = [&](int it0) {
+            uint4 vt[NB], vd[NB];
+            if (tr_on) {
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int it0 = (2 * h + ph) * 8;
-                    if (has_tr) {
-#pragma unroll 8
-                        for (int it = it0; it < it0 + 8; ++it) store_tr(it);
-                    }
-                    if (has_dir) {
-#pragma unroll 4
-                        for (int it = it0; it < it0 + 8; ++it) store_dir(it);
-                    }
+                for (int u = 0; u < NB; ++u) vt[u] = tr_read(it0 + u);
+            }
+            if (dir_on) {
+#pragma unroll
+                for (int u = 0; u < NB; ++u) {
+                    int64_t orow, ocol;
+                    vd[u] = gather(it0 + u, orow, ocol);
                 }
-            };
+            }
+            if (tr_on) {
+#pragma unroll
+                for (int u = 0; u < NB; ++u)
+                    __builtin_amdgcn_raw_buffer_store_b128(vec(vt[u]), r_tr, vo_tr, tr_soff(it0 + u), 0);
+            }
+            if (dir_on) {
+#pragma unroll
+                for (int u = 0; u < NB; ++u)
+                    __builtin_amdgcn_raw_buffer_store_b128(vec(vd[u]), r_dir, vo_dir, dir_soff(it0 + u), 0);
+            }
+        };
+        if constexpr (BM == 256) {
+            // Combine fragment rows 0-1 (tile rows y in [0, 64) and [128, 192),
+            // both wave rows), store those bands (pieces 0-7 and 16-23), then
+            // combine rows 2-3 while the first stores drain (pieces 8-15, 24-31).
+            static_assert(F == 4 && NT == 32 && NIT == 32, "band layout of the 256 tile");
             combine_row(0);
             combine_row(1);
             __syncthreads();
-            store_bands(0);
+            store_batch(0);
+            store_batch(16);
             combine_row(2);
             combine_row(3);
             __syncthreads();
-            store_bands(1);
-            split_done = true;
+            store_batch(8);
+            store_batch(24);
+        } else {
+            static_assert(NT == 8 && NIT == 8, "piece layout of the 128 tile");
+#pragma unroll
+            for (int a = 0; a < F; ++a) combine_row(a);
+            __syncthreads();
+            store_batch(0);
         }
+        return;
     }
-    if (split_done) return;
 
 #pragma unroll
     for (int a = 0; a < F; ++a) combine_row(a);
