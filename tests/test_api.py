@@ -6,6 +6,7 @@ and its branch classes (triton_adam.py:106-161, triton_muon.py:375-456).
 """
 
 import dataclasses
+import math
 import importlib
 
 import numpy as np
@@ -225,3 +226,41 @@ def test_capturable_flag():
     a._dev_steps = {torch.device("cpu"): torch.tensor(2.0)}  # as the first capturable step leaves it
     a.step()  # no gradient: the counter alone advances, where it lives
     assert a._dev_steps and a.step_num == 3
+
+
+def _brute_rounds(sizes, m, n, cus):
+    """Rounds of CU slots the grids of each group take, counted tile by tile."""
+    tile = 256 if m >= 2048 else 128
+    slots = cus * (1 if tile == 256 else 2)
+    tm, tn = -(-m // tile), -(-n // tile)
+    total = 0
+    for k in sizes:
+        sym = sum(1 for i in range(tm) for j in range(tm) if j >= i) * k
+        full = sum(1 for i in range(tm) for j in range(tn)) * k
+        total += math.ceil(sym / slots) * (n + m) + math.ceil(full / slots) * m
+    return total
+
+
+@pytest.mark.parametrize("count,cap,m,n", [
+    (96, 32, 4096, 14336), (96, 20, 4096, 14336), (64, 32, 4096, 4096), (64, 32, 1024, 4096),
+    (33, 32, 4096, 4096), (24, 32, 768, 3072), (1, 32, 768, 768), (7, 2, 2048, 2048), (40, 9, 1024, 1024)])
+def test_launch_group_sizes(count, cap, m, n):
+    """Group sizing: covers every matrix, respects the cap, splits near-evenly,
+    and never does worse than the plain even split under the cap."""
+    from triton_muon_adamw.muon.hip_muon import group_sizes
+    sizes = group_sizes(count, cap, m, n, 256)
+    assert sum(sizes) == count and max(sizes) <= cap and max(sizes) - min(sizes) <= 1
+    g = -(-count // cap)
+    even = [count // g + (1 if i < count % g else 0) for i in range(g)]
+    assert _brute_rounds(sizes, m, n, 256) <= _brute_rounds(even, m, n, 256)
+
+
+def test_launch_group_sizes_llama():
+    """The Llama-3-8B classes run as groups of 32 (whole rounds of 256 CUs for
+    the 136 symmetric tiles of a 4096-row Gram: 17 rounds for 32 matrices,
+    where 20 matrices take 11 rounds for 62.5% of the work)."""
+    from triton_muon_adamw.muon.hip_muon import group_sizes
+    assert group_sizes(96, 32, 4096, 14336, 256) == [32, 32, 32]
+    assert group_sizes(64, 32, 4096, 4096, 256) == [32, 32]
+    assert group_sizes(64, 32, 1024, 4096, 256) == [32, 32]
+    assert group_sizes(0, 32, 4096, 4096, 256) == []

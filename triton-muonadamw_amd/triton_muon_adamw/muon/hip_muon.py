@@ -200,6 +200,42 @@ def muon_step(weights: torch.Tensor, grad: torch.Tensor, momentum: torch.Tensor,
     _lib.check(st, "mamw_muon_step")
 
 
+def group_sizes(count: int, cap: int, m: int, n: int, cus: int) -> list[int]:
+    """Sizes of the launch groups for ``count`` matrices of one shape class
+    (``m = min(R, C)``, ``n = max(R, C)``), each at most ``cap``.
+
+    Every group runs its Gram, polynomial and update GEMMs as one grid each,
+    and a grid whose workgroups do not fill whole rounds of the GPU's
+    ``cus`` compute units leaves CUs idle in its last round.  The cost of a
+    group of k matrices is modelled as the rounds of each product times its
+    reduction length (Gram: n, polynomial and update: m), plus a quarter
+    round of each per group for its launches; among splits into g near-equal
+    groups for g from ceil(count / cap) up, the cheapest wins (ties: fewer
+    groups).  Tiles follow the library's choice (256 x 256 from m = 2048,
+    one workgroup per CU; else 128 x 128, two per CU).
+    """
+    if count <= 0:
+        return []
+    cap = max(1, min(cap, count))
+    tile = 256 if m >= 2048 else 128
+    slots = cus * (1 if tile == 256 else 2)
+    tm, tn = -(-m // tile), -(-n // tile)
+    sym, full = tm * (tm + 1) // 2, tm * tn
+
+    def cost(k: int) -> float:
+        rounds = lambda tiles: -(-tiles * k // slots)  # noqa: E731
+        return rounds(sym) * (n + m) + rounds(full) * m + 0.25 * (n + 2 * m)
+
+    best = None
+    g_min = -(-count // cap)
+    for g in range(g_min, min(count, g_min + 4) + 1):
+        sizes = [count // g + (1 if i < count % g else 0) for i in range(g)]
+        c = sum(cost(k) for k in sizes)
+        if best is None or c < best[0] - 1e-9:
+            best = (c, sizes)
+    return best[1]
+
+
 class _Call:
     """One batched ``mamw_muon_step`` launch group (matrices of one shape class)."""
 
@@ -213,9 +249,12 @@ class _Call:
 class HipMuon:
     """Muon over a list of 2-D parameters, batched by shape on gfx950."""
 
-    # Workspace per launch group is capped at this many bytes (the batch is
-    # split further when one group would need more).
-    workspace_limit_bytes = 8 << 30
+    # Workspace per launch group is capped at this many bytes (None: 1/20 of
+    # the device's memory, at most 16 GiB; on a 288 GB MI355X 14.4 GB, which
+    # lets the 4096 x 14336 Llama-8B matrices run in groups of 32 whose
+    # symmetric grids fill whole rounds of the 256 CUs: 3 ms per step faster
+    # than groups of 20).  Within the cap, group_sizes() picks the split.
+    workspace_limit_bytes: int | None = None
     # A step whose Newton-Schulz work (sum of ns_steps*(3 m^2 n + m^3)) is at
     # most this many flops runs its shape classes concurrently, one side
     # stream and one workspace each: their launches are too small to fill the
@@ -280,14 +319,19 @@ class HipMuon:
         need: dict = {}
         for gi, ((dev, m, n), plist) in enumerate(groups.items()):
             one = _workspace_bytes(1, m, n, self.steps)
-            cap = max(1, min(_lib.MUON_MAX_BATCH, self.workspace_limit_bytes // max(one, 1)))
-            n_sub = -(-len(plist) // cap)
-            per = -(-len(plist) // n_sub)
+            limit = self.workspace_limit_bytes
+            if limit is None:
+                limit = min(16 << 30, torch.cuda.get_device_properties(dev).total_memory // 20)
+            cap = max(1, min(_lib.MUON_MAX_BATCH, limit // max(one, 1)))
+            cus = torch.cuda.get_device_properties(dev).multi_processor_count
+            sizes = iter(group_sizes(len(plist), cap, m, n, cus))
+            per = next(sizes)
             chunks, cur, seen = [], [], set()
             for p in plist:  # a parameter listed twice goes to a later launch (launches are ordered)
                 if len(cur) == per or id(p) in seen:
                     chunks.append(cur)
                     cur, seen = [], set()
+                    per = next(sizes, per)
                 cur.append(p)
                 seen.add(id(p))
             chunks.append(cur)
