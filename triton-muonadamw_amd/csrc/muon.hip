@@ -7,14 +7,17 @@
 //                         unit of 32 x 128 parameter elements.
 //   2. muon_norm_kernel   fixed-order reduction of those partials ->
 //                         inv[b] = 1 / max(bf16(||X||_F), eps).
-//   3. muon_scale_kernel  X <- bf16(X * inv[b]) in place (torch's X.div_(norm)
-//                         rounding point) and XT = X^T.
+//   3. muon_scale_kernel  XT = bf16(X * inv[b])^T (torch's X.div_(norm)
+//                         rounding point).
 //   4. ns_steps x { GRAM: A = X X^T,  POLY: B = b A + c A A,  UPDATE: X = a X + B X }
-//      The last iteration's UPDATE is APPLY: its epilogue transposes back and
-//      writes param = param*(1-lr*wd) - slr*X.
-// All GEMMs are C = A_op * B_op^T over operands stored row-major with the
-// reduction index contiguous (X for the Gram, A for A A since A is symmetric,
-// B and XT for B X), so one MFMA tile kernel serves every product.
+//      with X held as XT only: the Gram reads XT k-major (LDS transpose reads)
+//      and UPDATE writes the next XT.  The last iteration's UPDATE is APPLY:
+//      its epilogue transposes back and writes param = param*(1-lr*wd) - slr*X.
+// All GEMMs are C = A_op * B_op^T over operands stored with the reduction
+// index contiguous (A for A A since A is symmetric, B and XT for B X), except
+// the Gram, whose operand XT has the reduction index as its row.  Workspace
+// matrices too large for 31-bit buffer offsets are row-major instead, and
+// there X itself is kept beside XT for a row-major Gram.
 #include <mutex>
 
 #include "mamw_device.h"
@@ -40,6 +43,26 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
     return __builtin_bit_cast(uint2, v);
 }
 
+// The same read issued as inline assembly, which the compiler's wait-count
+// pass does not see: the builtin's memory operand carries no alias scope, so
+// the pass would make every such read inside the GEMM loop wait for all LDS
+// DMA in flight (vmcnt(0)).  The caller waits for the result itself
+// (s_waitcnt lgkmcnt) before using it.
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+// `addr` is an LDS byte address, `off` a byte offset that must be a constant
+// once the caller is inlined and unrolled (it becomes the instruction's
+// immediate, 0..65535).
+__device__ __forceinline__ uint2 lds_read_tr16_untracked(uint32_t addr, int off) {
+    u32x2_t v;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(off));
+    return make_uint2(v.x, v.y);
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_ptr_t)(p)));
+}
+
 // ---------------------------------------------------------------------------
 // Prep: one tile of 64 x 128 parameter elements per block, two prep units
 // of 32 rows (parameter rows read in 512-byte runs; 64 x 64 tiles measured 6%
@@ -56,6 +79,7 @@ struct PrepArgs {
     float w_mom;    // 1 - beta   (lerp weight of the momentum update)
     float w_nest;   // beta       (lerp weight of the Nesterov blend)
     int xkb;        // workspace matrices are k-blocked
+    int scale_x;    // the scale kernel also writes X (the row-major Gram reads it)
     // Gradient-scaler step (NULL otherwise): gradients are divided by
     // *grad_scale; a non-zero *found_inf leaves the momentum (and, in the
     // apply kernels, the parameters) untouched.
@@ -237,7 +261,8 @@ __global__ __launch_bounds__(256) void muon_norm_kernel(const float* __restrict_
     }
 }
 
-// X <- bf16(X * inv[b]) in place and XT = X^T, one 128 x 64 tile of X per
+// XT = bf16(X * inv[b])^T (and X <- bf16(X * inv[b]) in place when scale_x),
+// one 128 x 64 tile of X per
 // block (two prep units), 16-byte global accesses throughout: in the k-blocked
 // layout the X tile is one contiguous 16 KB block and its transpose two 8 KB
 // ones.  Each thread scales a 4 x 8 block (rows 4rq..4rq+3, columns
@@ -265,7 +290,7 @@ __global__ __launch_bounds__(256) void muon_scale_kernel(const PrepArgs a, const
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
         v[p] = scale_bf16x8(v[p], s);
-        *reinterpret_cast<uint4*>(X + xoff(a.xkb, a.mp, a.np, i0 + 4 * rq + p, j0 + cg * 8)) = v[p];
+        if (a.scale_x) *reinterpret_cast<uint4*>(X + xoff(a.xkb, a.mp, a.np, i0 + 4 * rq + p, j0 + cg * 8)) = v[p];
     }
     uint2* t2 = reinterpret_cast<uint2*>(&tileT[0][0]);
 #pragma unroll
@@ -288,16 +313,17 @@ __global__ __launch_bounds__(256) void muon_scale_kernel(const PrepArgs a, const
     for (int k = 0; k < 4; ++k) dst[k] = tileT[tr][(4 * sq + k) ^ scale_swz(tr)];
 }
 
-// ns_steps == 0: the update is the normalised X itself.
+// ns_steps == 0: the update is the normalised X itself (read from X^T).
 __global__ __launch_bounds__(256) void muon_apply0_kernel(const MuonBatchDescs descs, const PrepArgs a, float keep) {
     if (a.found_inf && *a.found_inf != 0.0f) return;  // skipped gradient-scaler step
     const int bat = blockIdx.y;
     const MuonMatDesc& d = descs.d[bat];
-    const uint16_t* X = a.x + bat * a.mp * a.np;
+    const uint16_t* XT = a.xt + bat * a.mp * a.np;
     const int64_t total = d.rows * d.cols;
     for (int64_t e = int64_t(blockIdx.x) * 256 + threadIdx.x; e < total; e += int64_t(gridDim.x) * 256) {
         const int64_t r = e / d.cols, c = e % d.cols;
-        const float u = bf16_to_f32(d.tall ? X[xoff(a.xkb, a.mp, a.np, c, r)] : X[xoff(a.xkb, a.mp, a.np, r, c)]);
+        // X[i][j] = XT[j][i] with (i, j) = (c, r) for a tall parameter, (r, c) otherwise
+        const float u = bf16_to_f32(d.tall ? XT[xoff(a.xkb, a.np, a.mp, r, c)] : XT[xoff(a.xkb, a.np, a.mp, c, r)]);
         if (d.flags & MAMW_BF16_PARAM) {
             uint16_t* ph = reinterpret_cast<uint16_t*>(d.param);
             ph[e] = uint16_t(f32_to_bf16(__builtin_fmaf(-d.slr, u, bf16_to_f32(ph[e]) * keep)));
@@ -339,7 +365,7 @@ struct GemmArgs {
     int K;                // multiple of 64
     int tiles_m, tiles_n;
     int tiles_per_matrix; // tiles of one matrix in the launch (upper triangle when symmetric)
-    uint16_t* c;          // GRAM/POLY: symmetric output; UPDATE: X
+    uint16_t* c;          // GRAM/POLY: symmetric output; UPDATE: X (NULL: X^T only)
     int64_t c_bs, ldc;
     uint16_t* ct;         // UPDATE: X^T (may be NULL in the standalone entry)
     int64_t ct_bs, ldct;
@@ -351,6 +377,7 @@ struct GemmArgs {
     int64_t m, n;         // APPLY: valid extent of X
     int xkb;              // operands, coefficient and outputs k-blocked (xoff)
     const float* found_inf;  // APPLY: a non-zero *found_inf (skipped gradient-scaler step) writes nothing
+    int kmajor;           // GRAM, k-blocked: operands are X^T (lda = its rows), read k-major
 };
 
 // Launch block -> (matrix, tile row, tile col).
@@ -502,8 +529,9 @@ __device__ __forceinline__ void apply_end(const MuonMatDesc& d, const ApplyPiece
     }
 }
 
-template <int BM, int MODE, bool KB>
+template <int BM, int MODE, bool KB, bool KM = false>
 __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs g, const MuonBatchDescs descs) {
+    static_assert(!KM || (KB && MODE == MODE_GRAM), "k-major operands: the k-blocked Gram only");
     constexpr int BN = BM;
     constexpr int WT = BM / 2;              // wave tile edge
     constexpr int F = WT / 32;              // 32x32 fragments per wave edge
@@ -529,12 +557,19 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     // resource spans the tile's rows up to column K.
     constexpr bool KBOP = KB;
     const int64_t rows_a = int64_t(g.tiles_m) * BM, rows_b = int64_t(g.tiles_n) * BN;
-    const uint16_t* Ag = g.aop + bat * g.a_bs + int64_t(ti) * BM * (KBOP ? 64 : g.lda);
-    const uint16_t* Bg = g.bop + bat * g.b_bs + int64_t(tj) * BN * (KBOP ? 64 : g.ldb);
+    // KM: the operand is X^T (g.lda rows, k-blocked), and the tile's BM
+    // columns of it are BM/64 whole panels of g.lda rows x 128 bytes.
+    const uint16_t* Ag = KM ? g.aop + bat * g.a_bs + int64_t(ti) * (BM / 64) * g.lda * 64
+                            : g.aop + bat * g.a_bs + int64_t(ti) * BM * (KBOP ? 64 : g.lda);
+    const uint16_t* Bg = KM ? g.bop + bat * g.b_bs + int64_t(tj) * (BN / 64) * g.ldb * 64
+                            : g.bop + bat * g.b_bs + int64_t(tj) * BN * (KBOP ? 64 : g.ldb);
     const __amdgpu_buffer_rsrc_t ra =
-        make_rsrc(Ag, KBOP ? ((g.K / 64 - 1) * rows_a + BM) * 128 : ((BM - 1) * g.lda + g.K) * 2);
+        make_rsrc(Ag, KM ? (BM / 64) * g.lda * 128
+                         : KBOP ? ((g.K / 64 - 1) * rows_a + BM) * 128 : ((BM - 1) * g.lda + g.K) * 2);
     const __amdgpu_buffer_rsrc_t rb =
-        make_rsrc(Bg, KBOP ? ((g.K / 64 - 1) * rows_b + BN) * 128 : ((BN - 1) * g.ldb + g.K) * 2);
+        make_rsrc(Bg, KM ? (BN / 64) * g.ldb * 128
+                         : KBOP ? ((g.K / 64 - 1) * rows_b + BN) * 128 : ((BN - 1) * g.ldb + g.K) * 2);
+    const int pk2 = int(g.lda) * 128;  // KM: bytes per panel
     const int pa2 = int(rows_a) * 128, pb2 = int(rows_b) * 128;  // KBOP: bytes per k-step panel
 
     // Load i (0..LOADS-1) of an operand fills rows row0 = wave*BM/4 + 8i ..
@@ -544,9 +579,24 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     const int lda2 = KBOP ? 128 : int(g.lda) * 2, ldb2 = KBOP ? 128 : int(g.ldb) * 2;
     const int va0 = lrow * lda2 + (((lane & 7) ^ lrow) << 4), va1 = lrow * lda2 + (((lane & 7) ^ lrow ^ 1) << 4);
     const int vb0 = lrow * ldb2 + (((lane & 7) ^ lrow) << 4), vb1 = lrow * ldb2 + (((lane & 7) ^ lrow ^ 1) << 4);
+    // KM: an operand's stage is BM/64 panels of 64 k rows x 128 bytes, 1-KB
+    // block lc holding k rows (lc%8)*8.. of panel lc/8; a k row stores logical
+    // chunk c at physical chunk c ^ kswz, kswz = 4 for rows 2,3 (mod 4), so the
+    // transpose reads below (4 rows x 64 bytes per 32 lanes) are conflict free.
+    const int vk = lrow * 128 + (((lane & 7) ^ (((lrow >> 1) & 1) << 2)) << 4);
     // DMA number i: operand A for i < LOADS, else B.
     auto load1 = [&](int i, int k0, int buf) {
         const int ii = i % LOADS, row0 = wave * (BM / 4) + ii * 8;
+        if constexpr (KM) {
+            const int lc = wave * LOADS + ii;
+            uint16_t* dst = smem + buf * STAGE + (i < LOADS ? 0 : BM * kBK) + lc * 512;
+            const int soff = (lc >> 3) * pk2 + (k0 + (lc & 7) * 8) * 128;
+            if (i < LOADS)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)dst, 16, vk, soff, 0, 0);
+            else
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)dst, 16, vk, soff, 0, 0);
+            return;
+        }
         uint16_t* dst = smem + buf * STAGE + (i < LOADS ? 0 : BM * kBK) + row0 * kBK;
         if (i < LOADS)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)dst, 16, (ii & 1) ? va1 : va0,
@@ -555,6 +605,26 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_ptr_t)dst, 16, (ii & 1) ? vb1 : vb0,
                                                      row0 * ldb2 + (KBOP ? (k0 >> 6) * pb2 : k0 * 2), 0, 0);
     };
+    // KM fragment: two transpose reads of 4 k rows each.  In a 16-lane group
+    // lane s names k row (s/4) and columns 4(s%4).. of the group's 16 columns,
+    // so lane i receives column i at 4 consecutive k; lanes 16-31 take the next
+    // 16 columns, lanes 32-63 the rows 8 below.  km_o[b] is the lane's element
+    // offset inside its panel's k slice for a fragment at column 32b of it.
+    // km_base[side][b]: the lane's LDS byte address in stage buffer 0 for a
+    // fragment at column 32b of the first panel of this wave's rows (side 0,
+    // wm) or columns (side 1, wn); the rest is an immediate offset.
+    uint32_t km_base[2][2];
+    {
+        const int s = lane & 15, kx = ((s >> 3) & 1) << 2, lcl = 2 * ((lane >> 4) & 1) + ((s & 3) >> 1);
+        const int rowo = ((lane >> 5) * 8 + (s >> 2)) * 64 + (s & 1) * 4;
+        const int km_o[2] = {rowo + ((kx | lcl) << 3), rowo + (((4 ^ kx) | lcl) << 3)};
+        const uint32_t s0 = lds_addr(smem);
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            km_base[0][b] = s0 + ((wm * WT) >> 6) * 8192 + km_o[b] * 2;
+            km_base[1][b] = s0 + BM * kBK * 2 + ((wn * WT) >> 6) * 8192 + km_o[b] * 2;
+        }
+    }
     // Fragment read j of slice ks, in the order the MFMAs first use them
     // (a-major): fa0, fb0 .. fb[F-1], fa1 .. fa[F-1].
     auto read1 = [&](bf16x8_t (&fa)[F], bf16x8_t (&fb)[F], int buf, int ks, int j) {
@@ -562,6 +632,18 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         const int ch = ks * 2 + (lane >> 5);
         const bool isa = (j == 0) || (j > F);
         const int f = j == 0 ? 0 : (j <= F ? j - 1 : j - F);
+        if constexpr (KM) {
+            // column 32f of the wave's range: panel f/2, column half f%2
+            const uint32_t q = km_base[isa ? 0 : 1][f & 1] + uint32_t(buf) * (STAGE * 2);
+            const int off = (f >> 1) * 8192 + ks * 2048;
+            const uint2 lo = lds_read_tr16_untracked(q, off), hi = lds_read_tr16_untracked(q, off + 512);
+            const bf16x8_t v = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+            if (isa)
+                fa[f] = v;
+            else
+                fb[f] = v;
+            return;
+        }
         if (isa) {
             const int r = wm * WT + f * 32 + (lane & 31);
             fa[f] = *reinterpret_cast<const bf16x8_t*>(base + r * kBK + (lds_chunk(r, ch) << 3));
@@ -616,6 +698,16 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
                      bool reads, int rbuf, int rks, int loads, int k0, int lbuf, int llo, int lhi) {
 #pragma unroll
         for (int i = 0; i < NMF; ++i) {
+            if constexpr (KM) {
+                if (i == 0) {
+                    // (ca, cb) came from the untracked reads of the previous
+                    // slice: all of them are complete before its first MFMA
+                    // (waiting per MFMA for just its fragments, or spreading
+                    // the reads over all MFMAs, measured slower).
+                    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
             acc[i / F][i % F] =
                 __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[i / F], cb[i % F], acc[i / F][i % F], 0, 0, 0);
 #pragma unroll
@@ -791,7 +883,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     // A group covers 16 rows x 8 columns, the 4 groups of a wave adjacent
     // 8-column pieces of the same rows (2-way LDS bank conflicts at most);
     // piece `it` covers rows y in [16 (it / 2), +16) when BM = 256.
-    const bool has_dir = (SYM && !diag) || MODE == MODE_UPDATE || (MODE == MODE_APPLY && !tall);
+    const bool has_dir = (SYM && !diag) || (MODE == MODE_UPDATE && g.c) || (MODE == MODE_APPLY && !tall);
     constexpr int NXQ = BN / 32;                // 32-column pieces of a 16-row band
     constexpr int NIT = (BM / 16) * NXQ / 4;    // direct pieces per wave
     const int gi = lane & 15, grp = lane >> 4;
@@ -1020,6 +1112,13 @@ hipError_t launch_gemm(int tile, const GemmArgs& g, const MuonBatchDescs& d, int
     const bool kb = g.xkb != 0;
     const int32_t variant = 2 * tile + (kb ? 1 : 0);  // tile and the KB template flag
     const dim3 block(kGemmThreads);
+    if constexpr (MODE == MODE_GRAM) {
+        if (kb && g.kmajor) {
+            if (tile == 256)
+                return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, true, true>, grid, block, s, ga, d);
+            return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE, true, true>, grid, block, s, ga, d);
+        }
+    }
     if (kb) {
         if (tile == 256)
             return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, true>, grid, block, s, ga, d);
@@ -1041,6 +1140,14 @@ GemmArgs gram_args(const uint16_t* X, uint16_t* A, int64_t mp, int64_t kp, int t
     g.c_bs = mp * mp;
     g.ldc = mp;
     g.alpha = 1.f;
+    return g;
+}
+
+// A = X X^T from k-blocked XT (np x mp): both operands read k-major.
+GemmArgs gram_kmajor_args(const uint16_t* XT, uint16_t* A, int64_t mp, int64_t np, int tile) {
+    GemmArgs g = gram_args(XT, A, mp, np, tile);
+    g.lda = g.ldb = np;  // rows of X^T: the panel height
+    g.kmajor = 1;
     return g;
 }
 
@@ -1139,6 +1246,12 @@ int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double we
     // Workspace matrices k-blocked whenever a whole matrix's byte offsets fit the
     // 31-bit buffer offsets.
     pa.xkb = (p.mp * p.np * 2 < (int64_t(1) << 31)) ? 1 : 0;
+    // k-blocked: the Gram reads X^T k-major, so X is needed by nothing after
+    // the scale kernel and the updates write X^T only.  Row-major (matrices
+    // too large for 31-bit offsets): the Gram reads X, which every update
+    // writes beside X^T.
+    const bool kmajor = pa.xkb != 0;
+    pa.scale_x = kmajor ? 0 : 1;
     pa.grad_scale = grad_scale;
     pa.found_inf = found_inf;
     const double B = double(batch), m = double(p.m), n = double(p.n);
@@ -1153,10 +1266,10 @@ int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double we
     e = launch(K_MUON_NORM, 0, 0.0, 4.0 * B * double(p.prep_tiles), muon_norm_kernel, dim3(unsigned(batch)),
                dim3(256), s, static_cast<const float*>(part), p.prep_tiles, eps, inv);
     if (e != hipSuccess) return int(e);
-    // scale: read X; write X, XT (2 + 2 + 2 bytes per padded element), two prep units per block
+    // scale: read X; write XT (and X) (2 + 2 (+ 2) bytes per padded element), two prep units per block
     const dim3 sgrid(unsigned(p.prep_tiles / 2), unsigned(batch));
-    e = launch(K_MUON_SCALE, 0, 0.0, 6.0 * B * double(p.mp) * double(p.np), muon_scale_kernel, sgrid, dim3(256), s,
-               pa, static_cast<const float*>(inv));
+    e = launch(K_MUON_SCALE, 0, 0.0, (kmajor ? 4.0 : 6.0) * B * double(p.mp) * double(p.np), muon_scale_kernel,
+               sgrid, dim3(256), s, pa, static_cast<const float*>(inv));
     if (e != hipSuccess) return int(e);
 
     if (ns_steps == 0) {
@@ -1167,7 +1280,7 @@ int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double we
     int cur = 0;
     for (int it = 0; it < ns_steps; ++it) {
         const bool last = (it == ns_steps - 1);
-        GemmArgs gg = gram_args(X, A, p.mp, p.np, p.tile);
+        GemmArgs gg = kmajor ? gram_kmajor_args(XT[cur], A, p.mp, p.np, p.tile) : gram_args(X, A, p.mp, p.np, p.tile);
         gg.xkb = pa.xkb;
         e = launch_gemm<MODE_GRAM>(p.tile, gg, descs, batch, f_gram, s);
         if (e != hipSuccess) return int(e);
@@ -1175,7 +1288,8 @@ int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double we
         gp.xkb = pa.xkb;
         e = launch_gemm<MODE_POLY>(p.tile, gp, descs, batch, f_poly, s);
         if (e != hipSuccess) return int(e);
-        GemmArgs gu = update_args(Bm, XT[cur], X, last ? nullptr : XT[cur ^ 1], p.mp, p.np, p.tile, a);
+        GemmArgs gu = update_args(Bm, XT[cur], kmajor ? nullptr : X, last ? nullptr : XT[cur ^ 1], p.mp, p.np,
+                                  p.tile, a);
         gu.xkb = pa.xkb;
         if (last) {
             gu.found_inf = found_inf;
