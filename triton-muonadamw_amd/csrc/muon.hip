@@ -747,27 +747,37 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     if constexpr (MODE == MODE_GRAM) {
         // Steps 0..KT-2; step KT-2 loads the first half of the last step again,
         // into a buffer nothing reads any more (keeps the loop free of branches).
-        for (int kt = 0; kt < KT - 1; ++kt) {
-            const int buf = kt & 1;
+        auto gram_step = [&](int kt, int buf) {
             slice(fa0, fb0, fa1, fb1, true, buf, 1, 1, (kt + 1) * kBK, buf ^ 1, LH, NL);
             slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0, 0, 0);
             slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0, 0, 0);
             __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
             asm volatile("s_barrier" ::: "memory");
             slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, min(kt + 2, KT - 1) * kBK, buf, 0, LH);
+        };
+        // Two steps per iteration, so that each step's buffer is a constant
+        // and the fragment reads' addresses fold into immediate offsets.
+        int kt = 0;
+        for (; kt + 1 < KT - 1; kt += 2) {
+            gram_step(kt, 0);
+            gram_step(kt + 1, 1);
         }
+        if (kt < KT - 1) gram_step(kt, 0);
     } else {
         // Steps 0..KT-3, then step KT-2 (K is a multiple of 2 kBK: buffer 0).
         // Once step KT-2 releases buffer 0, it takes the first NPRE blocks of
         // the coefficient tile while step KT-1 runs from buffer 1.
-        for (int kt = 0; kt < KT - 2; ++kt) {
-            const int buf = kt & 1;
+        auto step = [&](int kt, int buf) {
             slice(fa0, fb0, fa1, fb1, true, buf, 1, 1, (kt + 1) * kBK, buf ^ 1, LH, NL);
             slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0, 0, 0);
             slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0, 0, 0);
             __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
             asm volatile("s_barrier" ::: "memory");
             slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, (kt + 2) * kBK, buf, 0, LH);
+        };
+        for (int kt = 0; kt < KT - 2; kt += 2) {  // KT - 2 is even
+            step(kt, 0);
+            step(kt + 1, 1);
         }
         slice(fa0, fb0, fa1, fb1, true, 0, 1, 1, (KT - 1) * kBK, 1, LH, NL);
         slice(fa1, fb1, fa0, fb0, true, 0, 2, 0, 0, 0, 0, 0);
