@@ -137,3 +137,42 @@ def test_llama8b_full_step_properties(gpu):
         err = ((u - ref.double()).norm() / ref.double().norm()).item()
         assert err <= 1e-2, f"{n}: update rel err {err} against torch's Newton-Schulz"
         del u, ref, mom, blend
+
+
+@pytest.mark.parametrize("shape", [(16384, 65536), (65536, 16384)])
+def test_rowmajor_workspace_path_vs_torch(gpu, shape):
+    """A matrix whose padded size is 2^31 bf16 bytes: the workspace matrices
+    are row-major (k-blocked byte offsets would need more than 31 bits), the
+    Gram reads X and every update writes X beside X^T.  Every GEMM launch of
+    the step must be the row-major variant, and the update must match torch's
+    Newton-Schulz on the same Nesterov blend (relative Frobenius error
+    <= 1e-2, computed in row chunks)."""
+    from triton_muon_adamw import _lib
+    from triton_muon_adamw.muon import HipMuon
+    gen = torch.Generator(device=gpu).manual_seed(11)
+    w0 = torch.empty(shape, device=gpu).normal_(0.0, 0.02, generator=gen)
+    p = torch.nn.Parameter(w0.clone())
+    p.grad = torch.empty(shape, device=gpu).normal_(0.0, 1e-3, generator=gen)
+    opt = HipMuon([p], lr=MC.lr, weight_decay=MC.weight_decay, coeffs=MC.coeffs, nesterov=MC.nesterov,
+                  beta=MC.beta, ns_steps=MC.ns_steps, eps=MC.eps)
+    _lib.prof_start()
+    opt.step()
+    torch.cuda.synchronize()
+    _lib.prof_stop()
+    recs = [r for r in _lib.prof_collect() if r["kernel"].startswith("ns_gemm")]
+    assert len(recs) == 3 * MC.ns_steps and all(r["variant"] & 1 == 0 for r in recs), recs
+    assert torch.isfinite(p).all()
+    keep = 1 - MC.lr * MC.weight_decay
+    adj = MC.lr * math.sqrt(max(1.0, shape[0] / shape[1]))
+    g = p.grad
+    blend = g.lerp(torch.zeros_like(g).lerp_(g, 1 - MC.beta), MC.beta)
+    ref = torch.optim._muon._zeropower_via_newtonschulz(blend, MC.coeffs, MC.ns_steps, MC.eps)
+    del blend
+    num = den = 0.0
+    for r0 in range(0, shape[0], 4096):
+        u = (w0[r0:r0 + 4096].double() * keep - p.detach()[r0:r0 + 4096].double()) / adj
+        rr = ref[r0:r0 + 4096].double()
+        num += ((u - rr) ** 2).sum().item()
+        den += (rr ** 2).sum().item()
+    err = math.sqrt(num / den)
+    assert err <= 1e-2, f"{shape}: update rel err {err} against torch's Newton-Schulz"
