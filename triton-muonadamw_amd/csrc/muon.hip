@@ -462,6 +462,27 @@ struct ApplyPiece {
     bool fast;     // p0 / p1 hold the loaded parameter
 };
 
+// NT: non-temporal parameter accesses (the parameter rows of a tall matrix,
+// written from whole tile columns: measured 4% faster on the 14336 x 4096
+// Llama-8B matrices; the wide matrices' row pieces measured 1.5% slower so).
+typedef unsigned int nt_u32x4_t __attribute__((ext_vector_type(4)));
+template <bool NT = false>
+__device__ __forceinline__ uint4 load_u4(const uint4* q) {
+    if constexpr (NT) {
+        const nt_u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4_t*>(q));
+        return make_uint4(v.x, v.y, v.z, v.w);
+    }
+    return *q;
+}
+template <bool NT = false>
+__device__ __forceinline__ void store_u4(uint4* q, uint4 w) {
+    if constexpr (NT)
+        __builtin_nontemporal_store(nt_u32x4_t{w.x, w.y, w.z, w.w}, reinterpret_cast<nt_u32x4_t*>(q));
+    else
+        *q = w;
+}
+
+template <bool NT = false>
 __device__ __forceinline__ void apply_begin(const MuonMatDesc& d, ApplyPiece& a, int64_t prow, int64_t pcol,
                                             int64_t cap, int64_t left) {
     const int64_t nv = cap < left ? cap : left;
@@ -474,11 +495,12 @@ __device__ __forceinline__ void apply_begin(const MuonMatDesc& d, ApplyPiece& a,
     a.fast = a.nv == 8 && ((pa | ua) & 15) == 0;
     if (a.fast) {
         const uint4* q = reinterpret_cast<const uint4*>(pa);
-        a.p0 = q[0];
-        if (!bf) a.p1 = q[1];
+        a.p0 = load_u4<NT>(q);
+        if (!bf) a.p1 = load_u4<NT>(q + 1);
     }
 }
 
+template <bool NT = false>
 __device__ __forceinline__ void apply_end(const MuonMatDesc& d, const ApplyPiece& a, float keep) {
     if (a.nv == 0) return;
     const uint32_t ww[4] = {a.w.x, a.w.y, a.w.z, a.w.w};
@@ -498,15 +520,17 @@ __device__ __forceinline__ void apply_end(const MuonMatDesc& d, const ApplyPiece
                 o[j] = pack_bf16x2(__builtin_fmaf(-d.slr, u[2 * j], bf16_to_f32(pv[j] & 0xffffu) * keep),
                                    __builtin_fmaf(-d.slr, u[2 * j + 1], bf16_to_f32(pv[j] >> 16) * keep));
             uint16_t* ph = reinterpret_cast<uint16_t*>(d.param) + a.idx;
-            *reinterpret_cast<uint4*>(ph) = make_uint4(o[0], o[1], o[2], o[3]);
+            store_u4<NT>(reinterpret_cast<uint4*>(ph), make_uint4(o[0], o[1], o[2], o[3]));
         } else {
             const uint32_t pv[8] = {a.p0.x, a.p0.y, a.p0.z, a.p0.w, a.p1.x, a.p1.y, a.p1.z, a.p1.w};
             float o[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) o[j] = __builtin_fmaf(-d.slr, u[j], __uint_as_float(pv[j]) * keep);
-            float4* p = reinterpret_cast<float4*>(d.param + a.idx);
-            p[0] = make_float4(o[0], o[1], o[2], o[3]);
-            p[1] = make_float4(o[4], o[5], o[6], o[7]);
+            uint4* p = reinterpret_cast<uint4*>(d.param + a.idx);
+            store_u4<NT>(p, make_uint4(__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]),
+                                       __float_as_uint(o[3])));
+            store_u4<NT>(p + 1, make_uint4(__float_as_uint(o[4]), __float_as_uint(o[5]), __float_as_uint(o[6]),
+                                           __float_as_uint(o[7])));
         }
         if (up) {
             reinterpret_cast<float4*>(up)[0] = make_float4(u[0], u[1], u[2], u[3]);
@@ -1044,11 +1068,11 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
                     const int k = (it0 + u) * kGemmThreads + tid;
                     const int x = k / NCH, c = k % NCH;
                     const int64_t orow = int64_t(tj) * BN + x, ocol = int64_t(ti) * BM + c * 8;
-                    apply_begin(d, pc[u], orow, ocol, orow < g.n ? int64_t(8) : int64_t(0), g.m - ocol);
+                    apply_begin<true>(d, pc[u], orow, ocol, orow < g.n ? int64_t(8) : int64_t(0), g.m - ocol);
                     pc[u].w = *reinterpret_cast<const uint4*>(TT + x * BM + (((c ^ x ^ (x >> 3)) & (NCH - 1)) << 3));
                 }
 #pragma unroll
-                for (int u = 0; u < U; ++u) apply_end(d, pc[u], g.keep);
+                for (int u = 0; u < U; ++u) apply_end<true>(d, pc[u], g.keep);
             }
         } else {
 #pragma unroll 8
@@ -1287,6 +1311,13 @@ int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double we
                           dim3(256), s, descs, pa, keep));
     }
     const double f_gram = B * m * m * n, f_poly = B * m * m * m, f_upd = 2.0 * B * m * m * n;
+    // The updates take 256 x 256 tiles from m = 1024 when the padded shape
+    // allows (each output element accumulates the same products in the same
+    // order under either tile, so the result does not depend on it): their
+    // grids hold mp/256 x np/256 tiles per matrix, enough to fill the GPU, and
+    // the larger tile halves the operand traffic per flop (1024 x 4096
+    // measured 11-13% faster; at m = 768 the 128 tile stays ahead).
+    const int utile = (p.tile == 128 && p.m >= 1024 && p.mp % 256 == 0 && p.np % 256 == 0) ? 256 : p.tile;
     int cur = 0;
     for (int it = 0; it < ns_steps; ++it) {
         const bool last = (it == ns_steps - 1);
@@ -1299,16 +1330,16 @@ int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double we
         e = launch_gemm<MODE_POLY>(p.tile, gp, descs, batch, f_poly, s);
         if (e != hipSuccess) return int(e);
         GemmArgs gu = update_args(Bm, XT[cur], kmajor ? nullptr : X, last ? nullptr : XT[cur ^ 1], p.mp, p.np,
-                                  p.tile, a);
+                                  utile, a);
         gu.xkb = pa.xkb;
         if (last) {
             gu.found_inf = found_inf;
             gu.keep = keep;
             gu.m = p.m;
             gu.n = p.n;
-            e = launch_gemm<MODE_APPLY>(p.tile, gu, descs, batch, f_upd, s);
+            e = launch_gemm<MODE_APPLY>(utile, gu, descs, batch, f_upd, s);
         } else {
-            e = launch_gemm<MODE_UPDATE>(p.tile, gu, descs, batch, f_upd, s);
+            e = launch_gemm<MODE_UPDATE>(utile, gu, descs, batch, f_upd, s);
         }
         if (e != hipSuccess) return int(e);
         cur ^= 1;
