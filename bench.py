@@ -56,7 +56,9 @@ def kernel_label(name: str, variant: int) -> str:
     """Demangled template name of a GEMM launch as rocprofv3 reports it."""
     if name.startswith("ns_gemm_kernel:"):
         mode = name.split(":")[1]
-        return f"ns_gemm_kernel<{variant // 2}, {MODE_NUM[mode]}, {'true' if variant % 2 else 'false'}>"
+        kb, km = variant & 1, (variant >> 1) & 1
+        return (f"ns_gemm_kernel<{variant // 4}, {MODE_NUM[mode]}, {'true' if kb else 'false'}, "
+                f"{'true' if km else 'false'}>")
     return name
 
 
@@ -492,6 +494,9 @@ def main():
     ap.add_argument("--calib-copy", action="store_true",
                     help="only copy 1 GiB three times (torch copy_): the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run")
+    ap.add_argument("--gpt2-in-order", action="store_true",
+                    help="only the GPT-2 (config 4) step with its Muon shape classes run in order (no side "
+                         "streams), for a kernel trace whose per-kernel durations do not overlap")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -512,6 +517,18 @@ def main():
             y.copy_(x)
         torch.cuda.synchronize()
         print(json.dumps({"calib_copy_bytes_each_way": x.numel() * 4, "copies": 3}), flush=True)
+        return
+    if args.gpt2_in_order:
+        from triton_muon_adamw import MuonAdamW
+
+        mc, ac = configs()
+        named = make_params(gpt2_layout(), dev, args.seed)
+        opt = MuonAdamW(split(named), muon_config=mc, adam_config=ac, parameter_split="explicit")
+        opt.muon.concurrent_flops_limit = 0.0
+        ms, wall, _ = time_steps(opt, args.steps, args.warmup)
+        print(json.dumps({"workload": "GPT-2 (config 4) MuonAdamW.step, Muon shape classes in order",
+                          "ms_per_step": round(ms, 4), "steps": args.steps, "warmup": args.warmup,
+                          "concurrent": opt.muon._concurrent}), flush=True)
         return
     layout = llama8b_layout()
     keep = None if args.no_cpu else llama_cpu_sample

@@ -1144,7 +1144,8 @@ hipError_t launch_gemm(int tile, const GemmArgs& g, const MuonBatchDescs& d, int
     const int32_t kid = MODE == MODE_GRAM ? K_NS_GRAM : MODE == MODE_POLY ? K_NS_POLY
                       : MODE == MODE_UPDATE ? K_NS_UPDATE : K_NS_APPLY;
     const bool kb = g.xkb != 0;
-    const int32_t variant = 2 * tile + (kb ? 1 : 0);  // tile and the KB template flag
+    const bool km = MODE == MODE_GRAM && kb && g.kmajor;
+    const int32_t variant = 4 * tile + (km ? 2 : 0) + (kb ? 1 : 0);  // tile and the KB, KM template flags
     const dim3 block(kGemmThreads);
     if constexpr (MODE == MODE_GRAM) {
         if (kb && g.kmajor) {
