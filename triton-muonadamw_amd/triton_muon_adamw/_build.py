@@ -106,11 +106,34 @@ def _compile(src: Path, obj: Path, verbose: bool) -> None:
             print("\n".join(lines), flush=True)
 
 
+def _check_untracked_reads(src: Path, verbose: bool, out_dir: Path = BUILD_DIR) -> None:
+    """Compile ``src``'s device code to assembly and verify its untracked LDS
+    reads (inline assembly the compiler's wait-count pass does not see): no
+    instruction may touch their registers before a wait that retires them."""
+    from . import _asmcheck
+
+    out = out_dir / (src.name + ".s")
+    cmd = [_hipcc(), *COMMON_FLAGS, *HIP_FLAGS[:-1], "-x", "hip", "--cuda-device-only", "-S", str(src),
+           "-o", str(out)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed on {src.name}:\n{res.stdout}\n{res.stderr}")
+    rep = _asmcheck.check(out.read_text())
+    if rep.untracked_reads == 0:
+        raise RuntimeError(f"{src.name}: no untracked LDS reads found in the GEMM kernels' assembly "
+                           "(the check would be vacuous)")
+    if rep.hazards:
+        raise RuntimeError(f"{src.name}: registers of untracked LDS reads used before their wait:\n"
+                           + "\n".join(rep.hazards[:20]))
+
+
 def build(verbose: bool = False) -> Path:
     """Compile every source and link the shared library; returns its path."""
     BUILD_DIR.mkdir(exist_ok=True)
     objs = []
-    jobs = min(len(SOURCES), max(1, os.cpu_count() or 1))
+    jobs = min(len(SOURCES) + 1, max(1, os.cpu_count() or 1))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = []
         for name in SOURCES:
@@ -118,6 +141,8 @@ def build(verbose: bool = False) -> Path:
             obj = BUILD_DIR / (name + ".o")
             objs.append(obj)
             futs.append(ex.submit(_compile, src, obj, verbose))
+            if "lds_read_tr16_untracked(" in src.read_text():
+                futs.append(ex.submit(_check_untracked_reads, src, verbose))
         for f in futs:
             f.result()
     tmp = LIB_PATH.with_name(LIB_NAME + ".tmp")
