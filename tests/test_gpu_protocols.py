@@ -13,6 +13,13 @@
 * ``adjust_lr_fn`` (triton_muon.py:424-431): ``"match_rms_adamw"`` against
   ``torch.optim.Muon`` with the same option; ``"spectral_unclamped"`` (which
   torch does not have) against the CPU oracle.
+* Mixed precision and LR schedules against torch: ``torch.amp.GradScaler``
+  driving this build (its device-side path) and, beside it, fused torch
+  AdamW + torch Muon (the scaler's unscale/skip path), with a non-finite step
+  that both skip; a ``LambdaLR`` schedule on this build and the same schedule
+  on the two torch optimizers.  AdamW parameters within 1e-6, every Muon
+  update within the reference tolerance of torch's (relative Frobenius error
+  <= 1e-2), step counters equal.
 """
 
 import copy
@@ -225,3 +232,99 @@ def test_adjust_lr_spectral_unclamped_against_oracle(gpu):
         assert rel_fro(got_u, exp_u) <= 1e-2, p0.shape
         # parameter differences are adj * (bf16 noise of the update), as in the oracle's own pin
         np.testing.assert_allclose(p.detach().cpu().numpy(), exp_p, atol=adj * 8e-3, rtol=0)
+
+
+# ---- GradScaler and LR schedules against the torch optimizers -----------------
+
+def _small_named(dev, seed):
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    lay = [(n, sh, b) for n, sh, b in gpt2_layout(n_layer=2, vocab=512) if not n.startswith("wpe")]
+    return [(n, nn.Parameter(torch.empty(sh, device=dev).normal_(0.0, 0.02, generator=gen)), b) for n, sh, b in lay]
+
+
+def _muon_updates_close(mine, theirs, before_m, before_t, mc, tag):
+    keep = 1 - mc.lr * mc.weight_decay
+    for (n, p, b), (_, q, _), p0, q0 in zip(mine, theirs, before_m, before_t):
+        if b != "muon":
+            continue
+        adj = mc.lr * math.sqrt(max(1.0, p.shape[0] / p.shape[1]))
+        u_m = (p0.double() * keep - p.detach().double()) / adj
+        u_t = (q0.double() * keep - q.detach().double()) / adj
+        err = ((u_m - u_t).norm() / u_t.norm()).item()
+        assert err <= 1e-2, f"{tag} {n}: update rel err {err}"
+
+
+def _adam_close(mine, theirs, tag):
+    for (n, p, b), (_, q, _) in zip(mine, theirs):
+        if b == "adam":
+            torch.testing.assert_close(p.detach(), q.detach(), atol=1e-6, rtol=0, msg=f"{tag} {n}")
+
+
+def test_grad_scaler_against_torch_optimizers(gpu):
+    mc = _mc()
+    mine, theirs = _small_named(gpu, 21), _small_named(gpu, 21)
+    opt = MuonAdamW(_split(mine), muon_config=mc, adam_config=AC, parameter_split="explicit")
+    ref = PyTorchMuonAdamW(_split(theirs), muon_config=mc, adam_config=AC, parameter_split="explicit")
+    s_m = torch.amp.GradScaler("cuda", init_scale=2048.0, growth_interval=1000)
+    s_t = torch.amp.GradScaler("cuda", init_scale=2048.0, growth_interval=1000)
+    for sc in (s_m, s_t):
+        sc.scale(torch.ones((), device=gpu))  # initialise the scale on the device
+    gen = torch.Generator(device=gpu).manual_seed(22)
+    for it in range(4):
+        grads = [torch.empty(p.shape, device=gpu).normal_(0.0, 1e-3, generator=gen) for _, p, _ in mine]
+        if it == 2:  # one non-finite gradient in each branch: every optimizer skips the step
+            grads[[k for k, (_, _, b) in enumerate(mine) if b == "adam"][0]].view(-1)[0] = float("inf")
+            grads[[k for k, (_, _, b) in enumerate(mine) if b == "muon"][0]].view(-1)[0] = float("nan")
+        scale = s_m.get_scale()
+        assert scale == s_t.get_scale()
+        for (_, p, _), (_, q, _), g in zip(mine, theirs, grads):
+            p.grad = g * scale
+            q.grad = g * scale
+        before_m = [p.detach().clone() for _, p, _ in mine]
+        before_t = [q.detach().clone() for _, q, _ in theirs]
+        s_m.step(opt)
+        s_m.update()
+        s_t.step(ref.adamw)
+        s_t.step(ref.muon)
+        s_t.update()
+        torch.cuda.synchronize()
+        if it == 2:
+            assert all(torch.equal(p.detach(), p0) for (_, p, _), p0 in zip(mine, before_m))
+            assert all(torch.equal(q.detach(), q0) for (_, q, _), q0 in zip(theirs, before_t))
+            continue
+        _adam_close(mine, theirs, f"step {it}")
+        _muon_updates_close(mine, theirs, before_m, before_t, mc, f"step {it}")
+    assert opt.adamw.step_num == 3
+    assert all(int(st["step"]) == 3 for st in ref.adamw.state.values())
+    assert s_m.get_scale() == s_t.get_scale() == 1024.0
+
+
+@pytest.mark.filterwarnings("ignore:Detected call of")
+def test_lr_schedule_against_torch_optimizers(gpu):
+    mc = _mc()
+    mine, theirs = _small_named(gpu, 31), _small_named(gpu, 31)
+    opt = MuonAdamW(_split(mine), muon_config=mc, adam_config=AC, parameter_split="explicit")
+    ref = PyTorchMuonAdamW(_split(theirs), muon_config=mc, adam_config=AC, parameter_split="explicit")
+    rate = lambda k: 0.6 ** k  # noqa: E731
+    sched = torch.optim.lr_scheduler.LambdaLR(opt, rate)
+    sched_a = torch.optim.lr_scheduler.LambdaLR(ref.adamw, rate)
+    sched_u = torch.optim.lr_scheduler.LambdaLR(ref.muon, rate)
+    gen = torch.Generator(device=gpu).manual_seed(32)
+    for k in range(4):
+        for (_, p, _), (_, q, _) in zip(mine, theirs):
+            g = torch.empty(p.shape, device=gpu).normal_(0.0, 1e-3, generator=gen)
+            p.grad, q.grad = g, g.clone()
+        before_m = [p.detach().clone() for _, p, _ in mine]
+        before_t = [q.detach().clone() for _, q, _ in theirs]
+        opt.step()
+        ref.step()
+        torch.cuda.synchronize()
+        _adam_close(mine, theirs, f"step {k}")
+        lr_k = mc.lr * rate(k)
+        _muon_updates_close(mine, theirs, before_m, before_t, MuonConfig(**{**mc.__dict__, "lr": lr_k}),
+                            f"step {k}")
+        sched.step()
+        sched_a.step()
+        sched_u.step()
+    assert math.isclose(opt.param_groups[1]["lr"], mc.lr * rate(4))
+    assert math.isclose(ref.muon.param_groups[0]["lr"], mc.lr * rate(4))
