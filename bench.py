@@ -56,9 +56,8 @@ def kernel_label(name: str, variant: int) -> str:
     """Demangled template name of a GEMM launch as rocprofv3 reports it."""
     if name.startswith("ns_gemm_kernel:"):
         mode = name.split(":")[1]
-        kb, km = variant & 1, (variant >> 1) & 1
-        return (f"ns_gemm_kernel<{variant // 4}, {MODE_NUM[mode]}, {'true' if kb else 'false'}, "
-                f"{'true' if km else 'false'}>")
+        flags = ["true" if (variant >> b) & 1 else "false" for b in range(3)]  # k-blocked, k-major, lower A
+        return f"ns_gemm_kernel<{variant // 8}, {MODE_NUM[mode]}, {', '.join(flags)}>"
     return name
 
 

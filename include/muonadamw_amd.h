@@ -270,7 +270,7 @@ int mamw_transpose_bf16(const uint16_t* src, uint16_t* dst, int batch,
  * runs under HIP graph capture.                                               */
 typedef struct mamw_prof_record {
     int32_t kernel;  /* see mamw_prof_kernel_name                                  */
-    int32_t variant; /* GEMMs: 4*tile + 2*(k-major operands) + (k-blocked); else 0 */
+    int32_t variant; /* GEMMs: 8*tile + 4*(A lower-triangle) + 2*(k-major) + (k-blocked) */
     double  flops;   /* algorithmic floating-point operations of the launch (0: n/a) */
     double  bytes;   /* algorithmic HBM bytes of the launch (0: not known here)      */
     float   ms;      /* dispatch duration                                            */

@@ -19,6 +19,7 @@
 // matrices too large for 31-bit buffer offsets are row-major instead, and
 // there X itself is kept beside XT for a row-major Gram.
 #include <mutex>
+#include <type_traits>
 
 #include "mamw_device.h"
 #include "mamw_launch.h"
@@ -378,6 +379,8 @@ struct GemmArgs {
     int xkb;              // operands, coefficient and outputs k-blocked (xoff)
     const float* found_inf;  // APPLY: a non-zero *found_inf (skipped gradient-scaler step) writes nothing
     int kmajor;           // GRAM, k-blocked: operands are X^T (lda = its rows), read k-major
+    int lower;            // GRAM/POLY, k-blocked: write only the lower triangle (the transposed orientation)
+    int a_low;            // UPDATE/APPLY, k-blocked: the A operand B holds only its lower triangle
 };
 
 // Launch block -> (matrix, tile row, tile col).
@@ -553,9 +556,13 @@ __device__ __forceinline__ void apply_end(const MuonMatDesc& d, const ApplyPiece
     }
 }
 
-template <int BM, int MODE, bool KB, bool KM = false>
-__global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs g, const MuonBatchDescs descs) {
+template <int BM, int MODE, bool KB, bool KM = false, bool LOWA = false>
+// 128 tiles: two workgroups per CU (64 KB of LDS and at most 256 registers
+// per lane each).
+__global__ __launch_bounds__(kGemmThreads, BM == 128 ? 2 : 1) void ns_gemm_kernel(const GemmArgs g,
+                                                                                 const MuonBatchDescs descs) {
     static_assert(!KM || (KB && MODE == MODE_GRAM), "k-major operands: the k-blocked Gram only");
+    static_assert(!LOWA || (KB && (MODE == MODE_UPDATE || MODE == MODE_APPLY)), "lower-triangle A: updates only");
     constexpr int BN = BM;
     constexpr int WT = BM / 2;              // wave tile edge
     constexpr int F = WT / 32;              // 32x32 fragments per wave edge
@@ -576,6 +583,12 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     }
     int bat, ti, tj;
     decode_tile<SYM>(g, bat, ti, tj);
+    // Uniform by construction; pinned to scalar registers so that every
+    // buffer resource derived from them is one (a resource the compiler
+    // cannot prove uniform turns each load into a loop over the lanes).
+    bat = __builtin_amdgcn_readfirstlane(bat);
+    ti = __builtin_amdgcn_readfirstlane(ti);
+    tj = __builtin_amdgcn_readfirstlane(tj);
     // Operand rows of the tile: row-major (row stride ld), or k-blocked (KB:
     // row stride 64 inside a 64-wide panel, panel stride rows*64).  The buffer
     // resource spans the tile's rows up to column K.
@@ -595,6 +608,17 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
                          : KBOP ? ((g.K / 64 - 1) * rows_b + BN) * 128 : ((BN - 1) * g.ldb + g.K) * 2);
     const int pk2 = int(g.lda) * 128;  // KM: bytes per panel
     const int pa2 = int(rows_a) * 128, pb2 = int(rows_b) * 128;  // KBOP: bytes per k-step panel
+    // LOWA: the A operand (B, mp x mp, symmetric) holds only its lower triangle
+    // of BM x BM blocks, so the tile's rows ti read block (ti, kb) row-major
+    // while kb < ti and block (kb, ti) k-major (rows k, columns i: B[k][i] =
+    // B[i][k]) after, through ra_km.  The diagonal block is stored whole and
+    // exactly symmetric, so it can be read either way: k-major for ti > 0,
+    // row-major for ti = 0.  The switch step ksw = max(ti, 1) BM/64 then
+    // leaves at least BM/64 steps on each side (the host uses LOWA only with
+    // two or more block rows), and the loop below needs no branches.
+    const int ksw = LOWA ? max(ti, 1) * (BM / 64) : 1 << 30;
+    const __amdgpu_buffer_rsrc_t ra_km =
+        make_rsrc(g.aop + bat * g.a_bs + int64_t(ti) * (BM / 64) * rows_a * 64, LOWA ? (BM / 64) * rows_a * 128 : 0);
 
     // Load i (0..LOADS-1) of an operand fills rows row0 = wave*BM/4 + 8i ..
     // row0+7: lane l lands at physical chunk l&7 of row row0 + l/8, which holds
@@ -609,8 +633,20 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     // transpose reads below (4 rows x 64 bytes per 32 lanes) are conflict free.
     const int vk = lrow * 128 + (((lane & 7) ^ (((lrow >> 1) & 1) << 2)) << 4);
     // DMA number i: operand A for i < LOADS, else B.
-    auto load1 = [&](int i, int k0, int buf) {
+    // lm (std::bool_constant, LOWA only): the A rows of the step loaded are
+    // k-major.  Both layouts put a load's 1 KB at the same LDS bytes
+    // (lc * 512 == row0 * kBK).
+    auto load1 = [&](int i, int k0, int buf, auto lm) __attribute__((always_inline)) {
         const int ii = i % LOADS, row0 = wave * (BM / 4) + ii * 8;
+        if constexpr (LOWA && decltype(lm)::value) {
+            if (i < LOADS) {
+                const int lc = wave * LOADS + ii;
+                uint16_t* dst = smem + buf * STAGE + lc * 512;
+                const int soff = __builtin_amdgcn_readfirstlane((lc >> 3) * pa2 + (k0 + (lc & 7) * 8) * 128);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_km, (lds_ptr_t)dst, 16, vk, soff, 0, 0);
+                return;
+            }
+        }
         if constexpr (KM) {
             const int lc = wave * LOADS + ii;
             uint16_t* dst = smem + buf * STAGE + (i < LOADS ? 0 : BM * kBK) + lc * 512;
@@ -651,11 +687,23 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     }
     // Fragment read j of slice ks, in the order the MFMAs first use them
     // (a-major): fa0, fb0 .. fb[F-1], fa1 .. fa[F-1].
-    auto read1 = [&](bf16x8_t (&fa)[F], bf16x8_t (&fb)[F], int buf, int ks, int j) {
+    // kma: the A side of this step is read k-major (KM, or LOWA above the
+    // diagonal); a std::bool_constant, so each call site compiles one path.
+    auto read1 = [&](bf16x8_t (&fa)[F], bf16x8_t (&fb)[F], int buf, int ks, int j, auto kma)
+                     __attribute__((always_inline)) {
         const uint16_t* base = smem + buf * STAGE;
         const int ch = ks * 2 + (lane >> 5);
         const bool isa = (j == 0) || (j > F);
         const int f = j == 0 ? 0 : (j <= F ? j - 1 : j - F);
+        if constexpr (!KM && decltype(kma)::value) {
+            if (isa) {
+                const uint32_t q = km_base[0][f & 1] + uint32_t(buf) * (STAGE * 2);
+                const int off = (f >> 1) * 8192 + ks * 2048;
+                const uint2 lo = lds_read_tr16_untracked(q, off), hi = lds_read_tr16_untracked(q, off + 512);
+                fa[f] = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                return;
+            }
+        }
         if constexpr (KM) {
             // column 32f of the wave's range: panel f/2, column half f%2
             const uint32_t q = km_base[isa ? 0 : 1][f & 1] + uint32_t(buf) * (STAGE * 2);
@@ -705,7 +753,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
                                                         : ((BN - 1) * g.lds + BM) * 2);
     const int lds2 = MODE == MODE_GRAM ? 0 : KB ? 128 : int(g.lds) * 2;  // bytes between TT rows' sources
     const int pnl2 = int(rows_t) * 128;                                   // KB: bytes per 64-column panel
-    auto src_load = [&](int b) {
+    auto src_load = [&](int b) __attribute__((always_inline)) {
         const int x0 = b * RPI, x = x0 + lane / NCH;
         const int c = ((lane % NCH) ^ x ^ (x >> 3)) & (NCH - 1);  // logical chunk at physical lane % NCH
         const int coff = KB ? (c >> 3) * pnl2 + (c & 7) * 16 : c * 16;
@@ -718,11 +766,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     // lbuf (1) or this wave's share of the coefficient blocks that fit in stage
     // buffer 0 (2).  All arguments are compile-time constants at every call, so
     // the body has no branches.
+    // kin: (ca, cb) came from untracked (k-major) reads; kma: the A reads
+    // issued here are k-major (both std::bool_constant).
     auto slice = [&](const bf16x8_t (&ca)[F], const bf16x8_t (&cb)[F], bf16x8_t (&na)[F], bf16x8_t (&nb)[F],
-                     bool reads, int rbuf, int rks, int loads, int k0, int lbuf, int llo, int lhi) {
+                     bool reads, int rbuf, int rks, int loads, int k0, int lbuf, int llo, int lhi, auto kin,
+                     auto kma, auto lm) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NMF; ++i) {
-            if constexpr (KM) {
+            if constexpr (KM || decltype(kin)::value) {
                 if (i == 0) {
                     // (ca, cb) came from the untracked reads of the previous
                     // slice: all of them are complete before its first MFMA
@@ -736,14 +787,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
                 __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[i / F], cb[i % F], acc[i / F][i % F], 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < RPM; ++r)
-                if (reads && i * RPM + r < 2 * F) read1(na, nb, rbuf, rks, i * RPM + r);
+                if (reads && i * RPM + r < 2 * F) read1(na, nb, rbuf, rks, i * RPM + r, kma);
 #pragma unroll
             for (int l = 0; l < LPM; ++l)
                 if (loads == 2 && i * LPM + l < 2 * LOADS) src_load(wave * 2 * LOADS + i * LPM + l);
             if (loads == 1) {
                 const int nl = lhi - llo, j0 = llo + (i * nl) / NMF, j1 = llo + ((i + 1) * nl) / NMF;
 #pragma unroll
-                for (int j = j0; j < j1; ++j) load1(j, k0, lbuf);
+                for (int j = j0; j < j1; ++j) load1(j, k0, lbuf, lm);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -751,17 +802,22 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
 
     const int KT = g.K / kBK;
     constexpr int NL = 2 * LOADS, LH = LOADS;  // DMA loads per step; the half issued two steps ahead
+    auto prologue_loads = [&](auto lm) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < NL; ++i) load1(i, 0, 0);
-    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
-    asm volatile("s_barrier" ::: "memory");
-    if (KT > 1) {
+        for (int i = 0; i < NL; ++i) load1(i, 0, 0, lm);
+        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+        asm volatile("s_barrier" ::: "memory");
+        if (KT > 1) {
 #pragma unroll
-        for (int i = 0; i < LH; ++i) load1(i, kBK, 1);
-    }
+            for (int i = 0; i < LH; ++i) load1(i, kBK, 1, lm);
+        }
+    };
+    prologue_loads(std::false_type{});  // LOWA: steps 0 and 1 are below ksw
     bf16x8_t fa0[F], fb0[F], fa1[F], fb1[F];
+    if constexpr (!LOWA) {  // LOWA: each segment reads its first slice
 #pragma unroll
-    for (int j = 0; j < 2 * F; ++j) read1(fa0, fb0, 0, 0, j);
+        for (int j = 0; j < 2 * F; ++j) read1(fa0, fb0, 0, 0, j, std::false_type{});
+    }
     // Step kt reads buffer kt&1.  Buffer kt&1 ^ 1 has been free since the
     // barrier of step kt-1, whose last slice started the first half of step
     // kt+1 there; the first slice of step kt adds the second half.  Before the
@@ -771,13 +827,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
     if constexpr (MODE == MODE_GRAM) {
         // Steps 0..KT-2; step KT-2 loads the first half of the last step again,
         // into a buffer nothing reads any more (keeps the loop free of branches).
-        auto gram_step = [&](int kt, int buf) {
-            slice(fa0, fb0, fa1, fb1, true, buf, 1, 1, (kt + 1) * kBK, buf ^ 1, LH, NL);
-            slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0, 0, 0);
-            slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0, 0, 0);
+        constexpr std::bool_constant<KM> km{};
+        auto gram_step = [&](int kt, int buf) __attribute__((always_inline)) {
+            slice(fa0, fb0, fa1, fb1, true, buf, 1, 1, (kt + 1) * kBK, buf ^ 1, LH, NL, km, km, km);
+            slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0, 0, 0, km, km, km);
+            slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0, 0, 0, km, km, km);
             __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
             asm volatile("s_barrier" ::: "memory");
-            slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, min(kt + 2, KT - 1) * kBK, buf, 0, LH);
+            slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, min(kt + 2, KT - 1) * kBK, buf, 0, LH, km, km, km);
         };
         // Two steps per iteration, so that each step's buffer is a constant
         // and the fragment reads' addresses fold into immediate offsets.
@@ -791,31 +848,72 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         // Steps 0..KT-3, then step KT-2 (K is a multiple of 2 kBK: buffer 0).
         // Once step KT-2 releases buffer 0, it takes the first NPRE blocks of
         // the coefficient tile while step KT-1 runs from buffer 1.
-        auto step = [&](int kt, int buf) {
-            slice(fa0, fb0, fa1, fb1, true, buf, 1, 1, (kt + 1) * kBK, buf ^ 1, LH, NL);
-            slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0, 0, 0);
-            slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0, 0, 0);
+        // cur: the A side of this step is read k-major; nxt: that of the next
+        // step, whose first slice this step's last slice reads; la: the A side
+        // of step kt+2, which the last slice loads (the first slice loads the
+        // B side of step kt+1), is k-major.
+        auto step = [&](int kt, int buf, auto cur, auto nxt, auto la) __attribute__((always_inline)) {
+            slice(fa0, fb0, fa1, fb1, true, buf, 1, 1, (kt + 1) * kBK, buf ^ 1, LH, NL, cur, cur, cur);
+            slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0, 0, 0, cur, cur, cur);
+            slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0, 0, 0, cur, cur, cur);
             __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
             asm volatile("s_barrier" ::: "memory");
-            slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, (kt + 2) * kBK, buf, 0, LH);
+            slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, (kt + 2) * kBK, buf, 0, LH, cur, nxt, la);
         };
-        for (int kt = 0; kt < KT - 2; kt += 2) {  // KT - 2 is even
-            step(kt, 0);
-            step(kt + 1, 1);
+        // The last two steps: step KT-2 (buffer 0) prefetches the coefficient
+        // tile into buffer 0 in its last slice while step KT-1 runs from buffer 1.
+        auto tail = [&](auto m) __attribute__((always_inline)) {
+            slice(fa0, fb0, fa1, fb1, true, 0, 1, 1, (KT - 1) * kBK, 1, LH, NL, m, m, m);
+            slice(fa1, fb1, fa0, fb0, true, 0, 2, 0, 0, 0, 0, 0, m, m, m);
+            slice(fa0, fb0, fa1, fb1, true, 0, 3, 0, 0, 0, 0, 0, m, m, m);
+            __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+            asm volatile("s_barrier" ::: "memory");
+            slice(fa1, fb1, fa0, fb0, true, 1, 0, 2, 0, 0, 0, 0, m, m, m);
+            slice(fa0, fb0, fa1, fb1, true, 1, 1, 0, 0, 0, 0, 0, m, m, m);
+            slice(fa1, fb1, fa0, fb0, true, 1, 2, 0, 0, 0, 0, 0, m, m, m);
+            slice(fa0, fb0, fa1, fb1, true, 1, 3, 0, 0, 0, 0, 0, m, m, m);
+            slice(fa1, fb1, fa0, fb0, false, 0, 0, 0, 0, 0, 0, 0, m, m, m);
+        };
+        constexpr std::false_type rm{};  // row-major A reads
+        constexpr std::true_type kmr{};  // k-major A reads
+        if constexpr (!LOWA) {
+            for (int kt = 0; kt < KT - 2; kt += 2) {  // KT - 2 is even
+                step(kt, 0, rm, rm, rm);
+                step(kt + 1, 1, rm, rm, rm);
+            }
+            tail(rm);
+        } else {
+            // Steps [0, ksw) row-major, then [ksw, KT) k-major; ksw is a
+            // multiple of BM/64, so pairs keep their buffers.  The last
+            // row-major pair loads the A sides of steps ksw and ksw+1, and its
+            // last slice reads step ksw's first slice as row-major (discarded:
+            // the k-major segment reads it again; the addresses are inside the
+            // stage buffer).
+#pragma unroll
+            for (int j = 0; j < 2 * F; ++j) read1(fa0, fb0, 0, 0, j, rm);
+            for (int kt = 0; kt < ksw - 2; kt += 2) {
+                step(kt, 0, rm, rm, rm);
+                step(kt + 1, 1, rm, rm, rm);
+            }
+            step(ksw - 2, 0, rm, rm, kmr);
+            step(ksw - 1, 1, rm, rm, kmr);
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): those reads are done before ...
+#pragma unroll
+            for (int j = 0; j < 2 * F; ++j) read1(fa0, fb0, 0, 0, j, kmr);  // ... these rewrite fa0, fb0
+            for (int kt = ksw; kt < KT - 2; kt += 2) {
+                step(kt, 0, kmr, kmr, kmr);
+                step(kt + 1, 1, kmr, kmr, kmr);
+            }
+            tail(kmr);
         }
-        slice(fa0, fb0, fa1, fb1, true, 0, 1, 1, (KT - 1) * kBK, 1, LH, NL);
-        slice(fa1, fb1, fa0, fb0, true, 0, 2, 0, 0, 0, 0, 0);
-        slice(fa0, fb0, fa1, fb1, true, 0, 3, 0, 0, 0, 0, 0);
-        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
-        asm volatile("s_barrier" ::: "memory");
-        slice(fa1, fb1, fa0, fb0, true, 1, 0, 2, 0, 0, 0, 0);
     }
-    {
+    if constexpr (MODE == MODE_GRAM) {  // the Gram's last step
+        constexpr std::bool_constant<KM> km{};
         const int buf = (KT - 1) & 1;
-        slice(fa0, fb0, fa1, fb1, true, buf, 1, 0, 0, 0, 0, 0);
-        slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0, 0, 0);
-        slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0, 0, 0);
-        slice(fa1, fb1, fa0, fb0, false, 0, 0, 0, 0, 0, 0, 0);
+        slice(fa0, fb0, fa1, fb1, true, buf, 1, 0, 0, 0, 0, 0, km, km, km);
+        slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0, 0, 0, km, km, km);
+        slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0, 0, 0, km, km, km);
+        slice(fa1, fb1, fa0, fb0, false, 0, 0, 0, 0, 0, 0, 0, km, km, km);
     }
     __builtin_amdgcn_s_waitcnt(0x0070);  // no DMA outlives the loop
 
@@ -967,7 +1065,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void ns_gemm_kernel(const GemmArgs
         const int vo_tr = tid * 16, vo_dir = (lane & 15) * 128 + (lane >> 4) * 16;
         const int base_tr = int((int64_t(ti) * (BM / 64) * rows_t + int64_t(tj) * BN) * 128);
         const int base_dir = int((int64_t(tj) * (BN / 64) * rows_x + int64_t(ti) * BM) * 128);
-        const bool tr_on = has_tr, dir_on = has_dir;
+        // lower: a symmetric product keeps only its lower triangle (the
+        // transposed orientation of the tiles on and above the diagonal).
+        const bool tr_on = has_tr, dir_on = has_dir && !(SYM && g.lower);
         auto tr_read = [&](int it) {
             const int x = (it % XP) * 32 + (tid >> 3), c = (it / XP) * 8 + (tid & 7);
             return *reinterpret_cast<const uint4*>(TT + x * BM + (((c ^ x ^ (x >> 3)) & (NCH - 1)) << 3));
@@ -1145,8 +1245,19 @@ hipError_t launch_gemm(int tile, const GemmArgs& g, const MuonBatchDescs& d, int
                       : MODE == MODE_UPDATE ? K_NS_UPDATE : K_NS_APPLY;
     const bool kb = g.xkb != 0;
     const bool km = MODE == MODE_GRAM && kb && g.kmajor;
-    const int32_t variant = 4 * tile + (km ? 2 : 0) + (kb ? 1 : 0);  // tile and the KB, KM template flags
+    const bool lowa = (MODE == MODE_UPDATE || MODE == MODE_APPLY) && kb && g.a_low;
+    // tile and the KB, KM, LOWA template flags
+    const int32_t variant = 8 * tile + (lowa ? 4 : 0) + (km ? 2 : 0) + (kb ? 1 : 0);
     const dim3 block(kGemmThreads);
+    if constexpr (MODE == MODE_UPDATE || MODE == MODE_APPLY) {
+        if (lowa) {
+            if (tile == 256)
+                return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, true, false, true>, grid, block, s,
+                              ga, d);
+            return launch(kid, variant, flops, 0.0, ns_gemm_kernel<128, MODE, true, false, true>, grid, block, s, ga,
+                          d);
+        }
+    }
     if constexpr (MODE == MODE_GRAM) {
         if (kb && g.kmajor) {
             if (tile == 256)
@@ -1319,6 +1430,12 @@ int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double we
     // the larger tile halves the operand traffic per flop (1024 x 4096
     // measured 11-13% faster; at m = 768 the 128 tile stays ahead).
     const int utile = (p.tile == 128 && p.m >= 1024 && p.mp % 256 == 0 && p.np % 256 == 0) ? 256 : p.tile;
+    // B = bA + cAA is written as its lower triangle only (the symmetric
+    // products' cheaper orientation), and the updates read the blocks above
+    // the diagonal transposed; needs the k-blocked layout and one tile size
+    // for both products (the blocks of B are the updates' k blocks), and at
+    // least two block rows.
+    const bool lower = kmajor && utile == p.tile && p.mp >= 2 * p.tile;
     int cur = 0;
     for (int it = 0; it < ns_steps; ++it) {
         const bool last = (it == ns_steps - 1);
@@ -1328,11 +1445,13 @@ int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double we
         if (e != hipSuccess) return int(e);
         GemmArgs gp = poly_args(A, Bm, p.mp, p.tile, b, c);
         gp.xkb = pa.xkb;
+        gp.lower = lower ? 1 : 0;
         e = launch_gemm<MODE_POLY>(p.tile, gp, descs, batch, f_poly, s);
         if (e != hipSuccess) return int(e);
         GemmArgs gu = update_args(Bm, XT[cur], kmajor ? nullptr : X, last ? nullptr : XT[cur ^ 1], p.mp, p.np,
                                   utile, a);
         gu.xkb = pa.xkb;
+        gu.a_low = lower ? 1 : 0;
         if (last) {
             gu.found_inf = found_inf;
             gu.keep = keep;
