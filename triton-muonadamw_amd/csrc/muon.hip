@@ -380,7 +380,7 @@ struct GemmArgs {
     const float* found_inf;  // APPLY: a non-zero *found_inf (skipped gradient-scaler step) writes nothing
     int kmajor;           // GRAM, k-blocked: operands are X^T (lda = its rows), read k-major
     int lower;            // GRAM/POLY, k-blocked: write only the lower triangle (the transposed orientation)
-    int a_low;            // UPDATE/APPLY, k-blocked: the A operand B holds only its lower triangle
+    int a_low;            // POLY/UPDATE/APPLY, k-blocked: the symmetric operand (A; B) holds only its lower triangle
 };
 
 // Launch block -> (matrix, tile row, tile col).
@@ -556,13 +556,16 @@ __device__ __forceinline__ void apply_end(const MuonMatDesc& d, const ApplyPiece
     }
 }
 
-template <int BM, int MODE, bool KB, bool KM = false, bool LOWA = false>
+template <int BM, int MODE, bool KB, bool KM = false, bool LOW = false>
 // 128 tiles: two workgroups per CU (64 KB of LDS and at most 256 registers
 // per lane each).
 __global__ __launch_bounds__(kGemmThreads, BM == 128 ? 2 : 1) void ns_gemm_kernel(const GemmArgs g,
                                                                                  const MuonBatchDescs descs) {
     static_assert(!KM || (KB && MODE == MODE_GRAM), "k-major operands: the k-blocked Gram only");
-    static_assert(!LOWA || (KB && (MODE == MODE_UPDATE || MODE == MODE_APPLY)), "lower-triangle A: updates only");
+    static_assert(!LOW || (KB && MODE != MODE_GRAM), "lower-triangle operands: polynomial and updates, k-blocked");
+    // LOW: the symmetric operand (A of the polynomial, both sides; B of the
+    // updates, side A) holds only its lower triangle of BM x BM blocks.
+    constexpr bool LOWA = LOW, LOWB = LOW && MODE == MODE_POLY;
     constexpr int BN = BM;
     constexpr int WT = BM / 2;              // wave tile edge
     constexpr int F = WT / 32;              // 32x32 fragments per wave edge
@@ -608,17 +611,21 @@ __global__ __launch_bounds__(kGemmThreads, BM == 128 ? 2 : 1) void ns_gemm_kerne
                          : KBOP ? ((g.K / 64 - 1) * rows_b + BN) * 128 : ((BN - 1) * g.ldb + g.K) * 2);
     const int pk2 = int(g.lda) * 128;  // KM: bytes per panel
     const int pa2 = int(rows_a) * 128, pb2 = int(rows_b) * 128;  // KBOP: bytes per k-step panel
-    // LOWA: the A operand (B, mp x mp, symmetric) holds only its lower triangle
-    // of BM x BM blocks, so the tile's rows ti read block (ti, kb) row-major
-    // while kb < ti and block (kb, ti) k-major (rows k, columns i: B[k][i] =
-    // B[i][k]) after, through ra_km.  The diagonal block is stored whole and
-    // exactly symmetric, so it can be read either way: k-major for ti > 0,
-    // row-major for ti = 0.  The switch step ksw = max(ti, 1) BM/64 then
-    // leaves at least BM/64 steps on each side (the host uses LOWA only with
-    // two or more block rows), and the loop below needs no branches.
-    const int ksw = LOWA ? max(ti, 1) * (BM / 64) : 1 << 30;
-    const __amdgpu_buffer_rsrc_t ra_km =
-        make_rsrc(g.aop + bat * g.a_bs + int64_t(ti) * (BM / 64) * rows_a * 64, LOWA ? (BM / 64) * rows_a * 128 : 0);
+    // A lower-triangle operand (LOWA / LOWB): the side's rows r (ti or tj)
+    // read block (r, kb) row-major while kb < r and block (kb, r) k-major
+    // after (rows k, columns r: S[k][r] = S[r][k]).  The diagonal block is
+    // stored whole and exactly symmetric, so it can be read either way:
+    // k-major for r > 0, row-major for r = 0.  The switch step
+    // ksw = max(r, 1) BM/64 then leaves at least BM/64 steps on each side (the
+    // host uses these layouts only with two or more block rows).  Loads pick
+    // their layout arithmetically from the step they load (no branches);
+    // fragment reads follow the loop segment they are in.
+    const int ksw_a = LOWA ? max(ti, 1) * (BM / 64) : 1 << 30;
+    const int ksw_b = LOWB ? max(tj, 1) * (BN / 64) : 1 << 30;
+    const __amdgpu_buffer_rsrc_t ra_low = make_rsrc(g.aop + bat * g.a_bs, LOWA ? rows_a * rows_a * 2 : 0);
+    const __amdgpu_buffer_rsrc_t rb_low = make_rsrc(g.bop + bat * g.b_bs, LOWB ? rows_b * rows_b * 2 : 0);
+    const int a_km_off = ti * (BM / 64) * pa2;  // tile offsets (bytes): A k-major, B in each layout
+    const int b_kb_off = tj * BN * 128, b_km_off = tj * (BN / 64) * pb2;
 
     // Load i (0..LOADS-1) of an operand fills rows row0 = wave*BM/4 + 8i ..
     // row0+7: lane l lands at physical chunk l&7 of row row0 + l/8, which holds
@@ -633,17 +640,34 @@ __global__ __launch_bounds__(kGemmThreads, BM == 128 ? 2 : 1) void ns_gemm_kerne
     // transpose reads below (4 rows x 64 bytes per 32 lanes) are conflict free.
     const int vk = lrow * 128 + (((lane & 7) ^ (((lrow >> 1) & 1) << 2)) << 4);
     // DMA number i: operand A for i < LOADS, else B.
-    // lm (std::bool_constant, LOWA only): the A rows of the step loaded are
-    // k-major.  Both layouts put a load's 1 KB at the same LDS bytes
-    // (lc * 512 == row0 * kBK).
-    auto load1 = [&](int i, int k0, int buf, auto lm) __attribute__((always_inline)) {
+    // Both layouts put a load's 1 KB at the same LDS bytes (lc * 512 ==
+    // row0 * kBK), so a lower-triangle side only switches the source address.
+    // la (std::bool_constant, LOWA): the A rows of the step loaded are k-major;
+    // every call site knows it.  The B side's switch step depends on the tile
+    // pair, so LOWB picks the layout arithmetically from the step loaded.
+    auto load1 = [&](int i, int k0, int buf, auto la) __attribute__((always_inline)) {
         const int ii = i % LOADS, row0 = wave * (BM / 4) + ii * 8;
-        if constexpr (LOWA && decltype(lm)::value) {
+        if constexpr (LOWA && decltype(la)::value) {
             if (i < LOADS) {
                 const int lc = wave * LOADS + ii;
                 uint16_t* dst = smem + buf * STAGE + lc * 512;
-                const int soff = __builtin_amdgcn_readfirstlane((lc >> 3) * pa2 + (k0 + (lc & 7) * 8) * 128);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_km, (lds_ptr_t)dst, 16, vk, soff, 0, 0);
+                const int soff =
+                    __builtin_amdgcn_readfirstlane(a_km_off + (lc >> 3) * pa2 + (k0 + (lc & 7) * 8) * 128);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra_low, (lds_ptr_t)dst, 16, vk, soff, 0, 0);
+                return;
+            }
+        }
+        if constexpr (LOWB) {
+            if (i >= LOADS) {
+                const int lc = wave * LOADS + ii;
+                uint16_t* dst = smem + buf * STAGE + BM * kBK + lc * 512;
+                const int f = 1 + ((k0 - ksw_b * kBK) >> 31);  // 1: k-major
+                const int s_rm = b_kb_off + row0 * 128 + (k0 >> 6) * pb2;
+                const int s_km = b_km_off + (lc >> 3) * pb2 + (k0 + (lc & 7) * 8) * 128;
+                const int soff = __builtin_amdgcn_readfirstlane(s_rm + f * (s_km - s_rm));
+                const int v_rm = (ii & 1) ? vb1 : vb0;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rb_low, (lds_ptr_t)dst, 16, v_rm + f * (vk - v_rm), soff, 0,
+                                                         0);
                 return;
             }
         }
@@ -687,20 +711,25 @@ __global__ __launch_bounds__(kGemmThreads, BM == 128 ? 2 : 1) void ns_gemm_kerne
     }
     // Fragment read j of slice ks, in the order the MFMAs first use them
     // (a-major): fa0, fb0 .. fb[F-1], fa1 .. fa[F-1].
-    // kma: the A side of this step is read k-major (KM, or LOWA above the
-    // diagonal); a std::bool_constant, so each call site compiles one path.
-    auto read1 = [&](bf16x8_t (&fa)[F], bf16x8_t (&fb)[F], int buf, int ks, int j, auto kma)
+    // kma, kmb: the A / B side of this step is read k-major (lower-triangle
+    // operands past their switch step); std::bool_constant, so each call
+    // site compiles one path.
+    auto read1 = [&](bf16x8_t (&fa)[F], bf16x8_t (&fb)[F], int buf, int ks, int j, auto kma, auto kmb)
                      __attribute__((always_inline)) {
         const uint16_t* base = smem + buf * STAGE;
         const int ch = ks * 2 + (lane >> 5);
         const bool isa = (j == 0) || (j > F);
         const int f = j == 0 ? 0 : (j <= F ? j - 1 : j - F);
-        if constexpr (!KM && decltype(kma)::value) {
-            if (isa) {
-                const uint32_t q = km_base[0][f & 1] + uint32_t(buf) * (STAGE * 2);
+        if constexpr (!KM && (decltype(kma)::value || decltype(kmb)::value)) {
+            if (isa ? decltype(kma)::value : decltype(kmb)::value) {
+                const uint32_t q = km_base[isa ? 0 : 1][f & 1] + uint32_t(buf) * (STAGE * 2);
                 const int off = (f >> 1) * 8192 + ks * 2048;
                 const uint2 lo = lds_read_tr16_untracked(q, off), hi = lds_read_tr16_untracked(q, off + 512);
-                fa[f] = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                const bf16x8_t v = __builtin_bit_cast(bf16x8_t, make_uint4(lo.x, lo.y, hi.x, hi.y));
+                if (isa)
+                    fa[f] = v;
+                else
+                    fb[f] = v;
                 return;
             }
         }
@@ -766,14 +795,14 @@ __global__ __launch_bounds__(kGemmThreads, BM == 128 ? 2 : 1) void ns_gemm_kerne
     // lbuf (1) or this wave's share of the coefficient blocks that fit in stage
     // buffer 0 (2).  All arguments are compile-time constants at every call, so
     // the body has no branches.
-    // kin: (ca, cb) came from untracked (k-major) reads; kma: the A reads
-    // issued here are k-major (both std::bool_constant).
+    // kma, kmb: this step's fragments are read k-major on the A / B side; then
+    // (ca, cb) came from untracked reads, which the first MFMA waits for.
     auto slice = [&](const bf16x8_t (&ca)[F], const bf16x8_t (&cb)[F], bf16x8_t (&na)[F], bf16x8_t (&nb)[F],
-                     bool reads, int rbuf, int rks, int loads, int k0, int lbuf, int llo, int lhi, auto kin,
-                     auto kma, auto lm) __attribute__((always_inline)) {
+                     bool reads, int rbuf, int rks, int loads, int k0, int lbuf, int llo, int lhi, auto kma,
+                     auto kmb, auto la) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NMF; ++i) {
-            if constexpr (KM || decltype(kin)::value) {
+            if constexpr (KM || decltype(kma)::value || decltype(kmb)::value) {
                 if (i == 0) {
                     // (ca, cb) came from the untracked reads of the previous
                     // slice: all of them are complete before its first MFMA
@@ -787,14 +816,14 @@ __global__ __launch_bounds__(kGemmThreads, BM == 128 ? 2 : 1) void ns_gemm_kerne
                 __builtin_amdgcn_mfma_f32_32x32x16_bf16(ca[i / F], cb[i % F], acc[i / F][i % F], 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < RPM; ++r)
-                if (reads && i * RPM + r < 2 * F) read1(na, nb, rbuf, rks, i * RPM + r, kma);
+                if (reads && i * RPM + r < 2 * F) read1(na, nb, rbuf, rks, i * RPM + r, kma, kmb);
 #pragma unroll
             for (int l = 0; l < LPM; ++l)
                 if (loads == 2 && i * LPM + l < 2 * LOADS) src_load(wave * 2 * LOADS + i * LPM + l);
             if (loads == 1) {
                 const int nl = lhi - llo, j0 = llo + (i * nl) / NMF, j1 = llo + ((i + 1) * nl) / NMF;
 #pragma unroll
-                for (int j = j0; j < j1; ++j) load1(j, k0, lbuf, lm);
+                for (int j = j0; j < j1; ++j) load1(j, k0, lbuf, la);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -802,21 +831,18 @@ __global__ __launch_bounds__(kGemmThreads, BM == 128 ? 2 : 1) void ns_gemm_kerne
 
     const int KT = g.K / kBK;
     constexpr int NL = 2 * LOADS, LH = LOADS;  // DMA loads per step; the half issued two steps ahead
-    auto prologue_loads = [&](auto lm) __attribute__((always_inline)) {
 #pragma unroll
-        for (int i = 0; i < NL; ++i) load1(i, 0, 0, lm);
-        __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
-        asm volatile("s_barrier" ::: "memory");
-        if (KT > 1) {
+    for (int i = 0; i < NL; ++i) load1(i, 0, 0, std::false_type{});  // steps 0, 1: below any switch
+    __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+    if (KT > 1) {
 #pragma unroll
-            for (int i = 0; i < LH; ++i) load1(i, kBK, 1, lm);
-        }
-    };
-    prologue_loads(std::false_type{});  // LOWA: steps 0 and 1 are below ksw
+        for (int i = 0; i < LH; ++i) load1(i, kBK, 1, std::false_type{});
+    }
     bf16x8_t fa0[F], fb0[F], fa1[F], fb1[F];
-    if constexpr (!LOWA) {  // LOWA: each segment reads its first slice
+    if constexpr (!LOW) {  // LOW: each loop segment reads its first slice
 #pragma unroll
-        for (int j = 0; j < 2 * F; ++j) read1(fa0, fb0, 0, 0, j, std::false_type{});
+        for (int j = 0; j < 2 * F; ++j) read1(fa0, fb0, 0, 0, j, std::bool_constant<KM>{}, std::bool_constant<KM>{});
     }
     // Step kt reads buffer kt&1.  Buffer kt&1 ^ 1 has been free since the
     // barrier of step kt-1, whose last slice started the first half of step
@@ -848,63 +874,90 @@ __global__ __launch_bounds__(kGemmThreads, BM == 128 ? 2 : 1) void ns_gemm_kerne
         // Steps 0..KT-3, then step KT-2 (K is a multiple of 2 kBK: buffer 0).
         // Once step KT-2 releases buffer 0, it takes the first NPRE blocks of
         // the coefficient tile while step KT-1 runs from buffer 1.
-        // cur: the A side of this step is read k-major; nxt: that of the next
-        // step, whose first slice this step's last slice reads; la: the A side
-        // of step kt+2, which the last slice loads (the first slice loads the
-        // B side of step kt+1), is k-major.
-        auto step = [&](int kt, int buf, auto cur, auto nxt, auto la) __attribute__((always_inline)) {
-            slice(fa0, fb0, fa1, fb1, true, buf, 1, 1, (kt + 1) * kBK, buf ^ 1, LH, NL, cur, cur, cur);
-            slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0, 0, 0, cur, cur, cur);
-            slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0, 0, 0, cur, cur, cur);
+        // ma, mb: the A / B fragments of this step are read k-major.  The last
+        // slice reads the next step's first slice the same way; at a switch
+        // of layout the next segment reads that slice again.
+        // la: the A side of step kt+2, which the last slice loads, is k-major
+        // (the first slice loads the B side of step kt+1).
+        auto step = [&](int kt, int buf, auto ma, auto mb, auto la) __attribute__((always_inline)) {
+            slice(fa0, fb0, fa1, fb1, true, buf, 1, 1, (kt + 1) * kBK, buf ^ 1, LH, NL, ma, mb, la);
+            slice(fa1, fb1, fa0, fb0, true, buf, 2, 0, 0, 0, 0, 0, ma, mb, la);
+            slice(fa0, fb0, fa1, fb1, true, buf, 3, 0, 0, 0, 0, 0, ma, mb, la);
             __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
             asm volatile("s_barrier" ::: "memory");
-            slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, (kt + 2) * kBK, buf, 0, LH, cur, nxt, la);
+            slice(fa1, fb1, fa0, fb0, true, buf ^ 1, 0, 1, (kt + 2) * kBK, buf, 0, LH, ma, mb, la);
         };
         // The last two steps: step KT-2 (buffer 0) prefetches the coefficient
         // tile into buffer 0 in its last slice while step KT-1 runs from buffer 1.
-        auto tail = [&](auto m) __attribute__((always_inline)) {
-            slice(fa0, fb0, fa1, fb1, true, 0, 1, 1, (KT - 1) * kBK, 1, LH, NL, m, m, m);
-            slice(fa1, fb1, fa0, fb0, true, 0, 2, 0, 0, 0, 0, 0, m, m, m);
-            slice(fa0, fb0, fa1, fb1, true, 0, 3, 0, 0, 0, 0, 0, m, m, m);
+        // (The tail loads no A side: ma stands in for la.)
+        auto tail = [&](auto ma, auto mb) __attribute__((always_inline)) {
+            slice(fa0, fb0, fa1, fb1, true, 0, 1, 1, (KT - 1) * kBK, 1, LH, NL, ma, mb, ma);
+            slice(fa1, fb1, fa0, fb0, true, 0, 2, 0, 0, 0, 0, 0, ma, mb, ma);
+            slice(fa0, fb0, fa1, fb1, true, 0, 3, 0, 0, 0, 0, 0, ma, mb, ma);
             __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
             asm volatile("s_barrier" ::: "memory");
-            slice(fa1, fb1, fa0, fb0, true, 1, 0, 2, 0, 0, 0, 0, m, m, m);
-            slice(fa0, fb0, fa1, fb1, true, 1, 1, 0, 0, 0, 0, 0, m, m, m);
-            slice(fa1, fb1, fa0, fb0, true, 1, 2, 0, 0, 0, 0, 0, m, m, m);
-            slice(fa0, fb0, fa1, fb1, true, 1, 3, 0, 0, 0, 0, 0, m, m, m);
-            slice(fa1, fb1, fa0, fb0, false, 0, 0, 0, 0, 0, 0, 0, m, m, m);
+            slice(fa1, fb1, fa0, fb0, true, 1, 0, 2, 0, 0, 0, 0, ma, mb, ma);
+            slice(fa0, fb0, fa1, fb1, true, 1, 1, 0, 0, 0, 0, 0, ma, mb, ma);
+            slice(fa1, fb1, fa0, fb0, true, 1, 2, 0, 0, 0, 0, 0, ma, mb, ma);
+            slice(fa0, fb0, fa1, fb1, true, 1, 3, 0, 0, 0, 0, 0, ma, mb, ma);
+            slice(fa1, fb1, fa0, fb0, false, 0, 0, 0, 0, 0, 0, 0, ma, mb, ma);
         };
-        constexpr std::false_type rm{};  // row-major A reads
-        constexpr std::true_type kmr{};  // k-major A reads
-        if constexpr (!LOWA) {
+        constexpr std::false_type rm{};  // row-major fragment reads
+        constexpr std::true_type kmr{};  // k-major fragment reads
+        if constexpr (!LOW) {
             for (int kt = 0; kt < KT - 2; kt += 2) {  // KT - 2 is even
                 step(kt, 0, rm, rm, rm);
                 step(kt + 1, 1, rm, rm, rm);
             }
-            tail(rm);
+            tail(rm, rm);
         } else {
-            // Steps [0, ksw) row-major, then [ksw, KT) k-major; ksw is a
-            // multiple of BM/64, so pairs keep their buffers.  The last
-            // row-major pair loads the A sides of steps ksw and ksw+1, and its
-            // last slice reads step ksw's first slice as row-major (discarded:
-            // the k-major segment reads it again; the addresses are inside the
-            // stage buffer).
+            // Segments [0, ksw_a): both sides row-major; [ksw_a, ksw_b): A
+            // k-major (the updates: to the end); [ksw_b, KT): both k-major.
+            // Each starts at an even step (buffer 0) by waiting for the reads in
+            // flight and reading its first slice in its own layout (the previous
+            // step's last slice read it in the old layout: discarded, and its
+            // addresses stay inside the stage buffer); the first segment is at
+            // least one pair long, the others may be empty.  The first
+            // segment's last pair loads the A sides of steps ksw_a, ksw_a+1,
+            // k-major; after it every A load is k-major.
+            auto segment = [&](int k_begin, int k_end, auto ma, auto mb, auto after) __attribute__((always_inline)) {
+                // Nothing may move above this wait: the registers of the reads
+                // still in flight are free to the compiler from here on.
+                __builtin_amdgcn_sched_barrier(0);
+                __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (decltype(after)::value) {
+                    // With both operands lower, the compiler may also reuse
+                    // those registers at the previous loop's exit: an empty
+                    // use after the wait keeps them live until it.
 #pragma unroll
-            for (int j = 0; j < 2 * F; ++j) read1(fa0, fb0, 0, 0, j, rm);
-            for (int kt = 0; kt < ksw - 2; kt += 2) {
-                step(kt, 0, rm, rm, rm);
-                step(kt + 1, 1, rm, rm, rm);
-            }
-            step(ksw - 2, 0, rm, rm, kmr);
-            step(ksw - 1, 1, rm, rm, kmr);
-            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): those reads are done before ...
+                    for (int f = 0; f < F; ++f) asm volatile("" ::"v"(fa0[f]), "v"(fb0[f]));
+                }
 #pragma unroll
-            for (int j = 0; j < 2 * F; ++j) read1(fa0, fb0, 0, 0, j, kmr);  // ... these rewrite fa0, fb0
-            for (int kt = ksw; kt < KT - 2; kt += 2) {
-                step(kt, 0, kmr, kmr, kmr);
-                step(kt + 1, 1, kmr, kmr, kmr);
+                for (int j = 0; j < 2 * F; ++j) read1(fa0, fb0, 0, 0, j, ma, mb);
+                if constexpr (decltype(ma)::value) {
+                    for (int kt = k_begin; kt < k_end; kt += 2) {
+                        step(kt, 0, ma, mb, kmr);
+                        step(kt + 1, 1, ma, mb, kmr);
+                    }
+                } else {
+                    for (int kt = k_begin; kt < k_end - 2; kt += 2) {
+                        step(kt, 0, ma, mb, rm);
+                        step(kt + 1, 1, ma, mb, rm);
+                    }
+                    step(k_end - 2, 0, ma, mb, kmr);
+                    step(k_end - 1, 1, ma, mb, kmr);
+                }
+            };
+            segment(0, ksw_a, rm, rm, std::false_type{});
+            if constexpr (LOWB) {
+                segment(ksw_a, ksw_b, kmr, rm, std::true_type{});
+                segment(ksw_b, KT - 2, kmr, kmr, std::true_type{});
+                tail(kmr, kmr);
+            } else {
+                segment(ksw_a, KT - 2, kmr, rm, std::false_type{});
+                tail(kmr, rm);
             }
-            tail(kmr);
         }
     }
     if constexpr (MODE == MODE_GRAM) {  // the Gram's last step
@@ -1245,12 +1298,12 @@ hipError_t launch_gemm(int tile, const GemmArgs& g, const MuonBatchDescs& d, int
                       : MODE == MODE_UPDATE ? K_NS_UPDATE : K_NS_APPLY;
     const bool kb = g.xkb != 0;
     const bool km = MODE == MODE_GRAM && kb && g.kmajor;
-    const bool lowa = (MODE == MODE_UPDATE || MODE == MODE_APPLY) && kb && g.a_low;
-    // tile and the KB, KM, LOWA template flags
-    const int32_t variant = 8 * tile + (lowa ? 4 : 0) + (km ? 2 : 0) + (kb ? 1 : 0);
+    const bool low = MODE != MODE_GRAM && kb && g.a_low;
+    // tile and the KB, KM, LOW template flags
+    const int32_t variant = 8 * tile + (low ? 4 : 0) + (km ? 2 : 0) + (kb ? 1 : 0);
     const dim3 block(kGemmThreads);
-    if constexpr (MODE == MODE_UPDATE || MODE == MODE_APPLY) {
-        if (lowa) {
+    if constexpr (MODE != MODE_GRAM) {
+        if (low) {
             if (tile == 256)
                 return launch(kid, variant, flops, 0.0, ns_gemm_kernel<256, MODE, true, false, true>, grid, block, s,
                               ga, d);
@@ -1430,22 +1483,24 @@ int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double we
     // the larger tile halves the operand traffic per flop (1024 x 4096
     // measured 11-13% faster; at m = 768 the 128 tile stays ahead).
     const int utile = (p.tile == 128 && p.m >= 1024 && p.mp % 256 == 0 && p.np % 256 == 0) ? 256 : p.tile;
-    // B = bA + cAA is written as its lower triangle only (the symmetric
-    // products' cheaper orientation), and the updates read the blocks above
-    // the diagonal transposed; needs the k-blocked layout and one tile size
-    // for both products (the blocks of B are the updates' k blocks), and at
-    // least two block rows.
+    // A = X X^T and B = bA + cAA are written as their lower triangles only
+    // (the symmetric products' cheaper orientation); the polynomial and the
+    // updates read the blocks above the diagonal transposed.  Needs the
+    // k-blocked layout, one tile size for all three products (the blocks of A
+    // and B are the next products' k blocks) and at least two block rows.
     const bool lower = kmajor && utile == p.tile && p.mp >= 2 * p.tile;
     int cur = 0;
     for (int it = 0; it < ns_steps; ++it) {
         const bool last = (it == ns_steps - 1);
         GemmArgs gg = kmajor ? gram_kmajor_args(XT[cur], A, p.mp, p.np, p.tile) : gram_args(X, A, p.mp, p.np, p.tile);
         gg.xkb = pa.xkb;
+        gg.lower = lower ? 1 : 0;
         e = launch_gemm<MODE_GRAM>(p.tile, gg, descs, batch, f_gram, s);
         if (e != hipSuccess) return int(e);
         GemmArgs gp = poly_args(A, Bm, p.mp, p.tile, b, c);
         gp.xkb = pa.xkb;
         gp.lower = lower ? 1 : 0;
+        gp.a_low = lower ? 1 : 0;
         e = launch_gemm<MODE_POLY>(p.tile, gp, descs, batch, f_poly, s);
         if (e != hipSuccess) return int(e);
         GemmArgs gu = update_args(Bm, XT[cur], kmajor ? nullptr : X, last ? nullptr : XT[cur ^ 1], p.mp, p.np,
