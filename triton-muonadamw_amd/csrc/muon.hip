@@ -391,9 +391,10 @@ struct GemmArgs {
 // 8 x 32 blocks, 32 consecutive logical tiles (a compact patch of one matrix
 // whose tiles share operand rows in that XCD's L2), and gives the 8 XCDs
 // neighbouring patches, so the round's operands are one matrix's worth and stay
-// in the memory-side cache.  Blocks of an incomplete last round keep their
-// index.  Logical order within a matrix: groups of kGroupM tile rows, column
-// by column (symmetric products: only the tiles with ti <= tj).
+// in the memory-side cache.  An incomplete last round (all of a grid smaller
+// than 8 x 32) is cut into 8 contiguous ranges, one per XCD.  Logical order
+// within a matrix: groups of kGroupM tile rows, column by column (symmetric
+// products: only the tiles with ti <= tj).
 constexpr int kXcds = 8;
 constexpr int kXcdSlots = 32;
 constexpr int kGroupM = 4;
@@ -403,7 +404,9 @@ __device__ __forceinline__ void decode_tile(const GemmArgs& g, int& bat, int& ti
     const int L = blockIdx.x, total = gridDim.x;
     const int full = (total / (kXcds * kXcdSlots)) * (kXcds * kXcdSlots);
     const int xcd = L % kXcds, j = L / kXcds;
-    const int logical = L < full ? ((j / kXcdSlots) * kXcds + xcd) * kXcdSlots + j % kXcdSlots : L;
+    const int rem = total - full, q = rem / kXcds, r = rem % kXcds;  // the last round: XCD x gets q or q+1
+    const int logical = L < full ? ((j / kXcdSlots) * kXcds + xcd) * kXcdSlots + j % kXcdSlots
+                                 : full + xcd * q + min(xcd, r) + (L - full) / kXcds;
     bat = logical / g.tiles_per_matrix;
     int t = logical - bat * g.tiles_per_matrix;
     const int T = g.tiles_m;
