@@ -205,8 +205,8 @@ int mamw_muon_step(const mamw_muon_matrix* mats, int batch, double lr,
  * hipMalloc/hipFree, and no profiler events even while profiling is on).
  * Limits and sharing:
  *   - a batch whose mamw_muon_workspace_bytes exceeds the array is rejected
- *     with MAMW_ERR_SCRATCH (one 4096 x 14336 matrix needs 400 MiB; what
- *     fits: 1 of 4096 x 4096, 9 of 1024 x 4096, 16 of 768 x 3072, 20 of
+ *     with MAMW_ERR_SCRATCH (one 4096 x 14336 matrix needs 288 MiB; what
+ *     fits: 1 of 4096 x 4096, 12 of 1024 x 4096, 22 of 768 x 3072, 28 of
  *     768 x 2304, 32 of 768 x 768);
  *   - every call on one GPU uses that GPU's one array, which keeps the last
  *     call's contents (nothing in it needs to start at zero: each step writes

@@ -131,12 +131,13 @@ int muon_plan(int batch, int64_t rows, int64_t cols, int ns_steps, MuonPlan* pla
     p.np = round_up(p.n, p.tile);
     if (p.mp * p.np > kMaxMatElems) return MAMW_ERR_SHAPE;
     p.prep_tiles = (p.mp / kPrepTile) * (p.np / kPrepTile);
+    p.xkb = (p.mp * p.np * 2 < (int64_t(1) << 31)) ? 1 : 0;
     const size_t B = size_t(batch);
     const size_t xe = size_t(p.mp) * size_t(p.np);  // elements of X / XT
     const size_t ae = size_t(p.mp) * size_t(p.mp);  // elements of A / B
     size_t off = 0;
     p.off_x = off;
-    off = align_ws(off + B * xe * 2);
+    if (!p.xkb) off = align_ws(off + B * xe * 2);
     p.off_xt0 = off;
     off = align_ws(off + B * xe * 2);
     p.off_xt1 = off;

@@ -84,6 +84,9 @@ struct MuonPlan {
     int tile;  // GEMM tile edge (128 or 256); mp, np are multiples of it
     int64_t m, n, mp, np;
     int64_t prep_tiles;  // prep units, (mp/64) * (np/64); the prep kernel takes two per block
+    int xkb;             // workspace matrices k-blocked: a whole matrix's byte offsets fit 31 bits
+    // X is kept only when !xkb (the row-major Gram reads it); otherwise its
+    // region is empty and off_x == off_xt0.
     size_t off_x, off_xt0, off_xt1, off_a, off_b, off_part, off_inv;
     size_t bytes;
 };

@@ -1,14 +1,15 @@
 // Muon step for gfx950: momentum -> Newton-Schulz (bf16 MFMA) -> update.
 //
 // Launch sequence for one batch of equal-shaped matrices (mamw_muon_step):
-//   1. muon_prep_kernel   momentum lerp, Nesterov blend, bf16 cast (tall
-//                         matrices transposed through LDS); writes X (m x n,
-//                         zero-padded) and one fp32 sum of squares per prep
-//                         unit of 32 x 128 parameter elements.
+//   1. muon_prep_kernel   momentum lerp, Nesterov blend, bf16 cast; writes
+//                         X^T (n x m, zero-padded: a tall parameter's rows
+//                         are X^T rows, a wide one is transposed through LDS)
+//                         and one fp32 sum of squares per prep unit of
+//                         32 x 128 parameter elements.
 //   2. muon_norm_kernel   fixed-order reduction of those partials ->
 //                         inv[b] = 1 / max(bf16(||X||_F), eps).
-//   3. muon_scale_kernel  XT = bf16(X * inv[b])^T (torch's X.div_(norm)
-//                         rounding point).
+//   3. muon_scale_kernel  XT = bf16(XT * inv[b]) in place (torch's
+//                         X.div_(norm) rounding point).
 //   4. ns_steps x { GRAM: A = X X^T,  POLY: B = b A + c A A,  UPDATE: X = a X + B X }
 //      with X held as XT only: the Gram reads XT k-major (LDS transpose reads)
 //      and UPDATE writes the next XT.  The last iteration's UPDATE is APPLY:
@@ -17,7 +18,8 @@
 // index contiguous (A for A A since A is symmetric, B and XT for B X), except
 // the Gram, whose operand XT has the reduction index as its row.  Workspace
 // matrices too large for 31-bit buffer offsets are row-major instead, and
-// there X itself is kept beside XT for a row-major Gram.
+// there X itself is kept beside XT for a row-major Gram: prep writes X and
+// the scale kernel writes both X and XT = bf16(X * inv[b])^T.
 #include <mutex>
 #include <type_traits>
 
@@ -80,7 +82,8 @@ struct PrepArgs {
     float w_mom;    // 1 - beta   (lerp weight of the momentum update)
     float w_nest;   // beta       (lerp weight of the Nesterov blend)
     int xkb;        // workspace matrices are k-blocked
-    int scale_x;    // the scale kernel also writes X (the row-major Gram reads it)
+    int xt_direct;  // prep writes X^T and the scale pass rescales it in place
+                    // (else prep writes X and the scale pass writes X and X^T)
     // Gradient-scaler step (NULL otherwise): gradients are divided by
     // *grad_scale; a non-zero *found_inf leaves the momentum (and, in the
     // apply kernels, the parameters) untouched.
@@ -111,7 +114,12 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
     const int64_t bands = tall ? a.mp / 128 : a.np / 128;  // 128-column pieces per parameter row band
     const int64_t r0 = (q / bands) * 64, c0 = (q % bands) * 128;  // tile origin in the parameter
     const int64_t R = d.rows, C = d.cols;
-    uint16_t* X = a.x + bat * a.mp * a.np;
+    // Output: X^T (np x mp) when xt_direct, else X (mp x np).  A parameter row
+    // is a row of X^T for a tall matrix (X = P^T) and a row of X for a wide
+    // one; the other case goes through the LDS transpose.
+    uint16_t* const out = a.xt_direct ? a.xt + bat * a.np * a.mp : a.x + bat * a.mp * a.np;
+    const int64_t orows = a.xt_direct ? a.np : a.mp, ocols = a.xt_direct ? a.mp : a.np;
+    const bool straight = a.xt_direct ? tall : !tall;
 
     // Thread tid covers 4 consecutive columns (cg) of rows rr + 8 * pass;
     // passes 0-3 are the first prep unit (rows 0-31), 4-7 the second.
@@ -213,8 +221,8 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
             const float xb = bf16_to_f32(h[e]);
             ss[pass >> 2] += xb * xb;
         }
-        if (!tall) {  // X = bf16(u): parameter rows are X rows
-            *reinterpret_cast<uint2*>(X + xoff(a.xkb, a.mp, a.np, r, c)) = pk;
+        if (straight) {  // parameter rows are rows of the output
+            *reinterpret_cast<uint2*>(out + xoff(a.xkb, orows, ocols, r, c)) = pk;
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) tileT[cg * 4 + e][rl] = uint16_t(h[e]);
@@ -230,13 +238,13 @@ __global__ __launch_bounds__(256) void muon_prep_kernel(const MuonBatchDescs des
         const int64_t unit = (2 * (q / bands) + tid) * bands + q % bands;
         a.part[bat * a.prep_tiles + unit] = (red[tid][0] + red[tid][1]) + (red[tid][2] + red[tid][3]);
     }
-    if (tall) {  // X = bf16(u)^T: row (c0 + tr) of X, 32 consecutive elements per thread
+    if (!straight) {  // output = bf16(u)^T: row (c0 + tr), 32 consecutive elements per thread
         const int tr = tid >> 1, seg = (tid & 1) * 32;
         uint32_t w[16];
 #pragma unroll
         for (int k = 0; k < 16; ++k)
             w[k] = uint32_t(tileT[tr][seg + 2 * k]) | (uint32_t(tileT[tr][seg + 2 * k + 1]) << 16);
-        uint4* dst = reinterpret_cast<uint4*>(X + xoff(a.xkb, a.mp, a.np, c0 + tr, r0 + seg));
+        uint4* dst = reinterpret_cast<uint4*>(out + xoff(a.xkb, orows, ocols, c0 + tr, r0 + seg));
 #pragma unroll
         for (int k = 0; k < 4; ++k) dst[k] = make_uint4(w[4 * k], w[4 * k + 1], w[4 * k + 2], w[4 * k + 3]);
     }
@@ -262,20 +270,33 @@ __global__ __launch_bounds__(256) void muon_norm_kernel(const float* __restrict_
     }
 }
 
-// XT = bf16(X * inv[b])^T (and X <- bf16(X * inv[b]) in place when scale_x),
-// one 128 x 64 tile of X per
-// block (two prep units), 16-byte global accesses throughout: in the k-blocked
-// layout the X tile is one contiguous 16 KB block and its transpose two 8 KB
-// ones.  Each thread scales a 4 x 8 block (rows 4rq..4rq+3, columns
-// 8cg..8cg+7) and writes its 8 columns to the LDS transpose as 8-byte runs of
-// 4 rows.  tileT row c (X column c) holds 128 elements as 16 chunks of 16
-// bytes, chunk k stored at k ^ scale_swz(c): the 8-byte column writes of 32
-// lanes and the 16-byte row reads of 16 lanes each touch every bank once
-// (2-byte writes into a padded tile measured 85% of the kernel's LDS cycles
-// in bank conflicts).
+// XT_ONLY (xt_direct): XT = bf16(XT * inv[b]) in place, a plain stream of
+// 16-byte pieces, four per thread (all loads before the stores), 8192
+// elements per block.
+// Otherwise (the row-major workspace): XT = bf16(X * inv[b])^T and
+// X <- bf16(X * inv[b]) in place, one 128 x 64 tile of X per block (two prep
+// units), 16-byte global accesses throughout.  Each thread scales a 4 x 8
+// block (rows 4rq..4rq+3, columns 8cg..8cg+7) and writes its 8 columns to the
+// LDS transpose as 8-byte runs of 4 rows.  tileT row c (X column c) holds 128
+// elements as 16 chunks of 16 bytes, chunk k stored at k ^ scale_swz(c): the
+// 8-byte column writes of 32 lanes and the 16-byte row reads of 16 lanes each
+// touch every bank once (2-byte writes into a padded tile measured 85% of the
+// kernel's LDS cycles in bank conflicts).
 __device__ __forceinline__ int scale_swz(int c) { return ((c >> 3) << 1) ^ (c & 3); }
 
+template <bool XT_ONLY>
 __global__ __launch_bounds__(256) void muon_scale_kernel(const PrepArgs a, const float* __restrict__ inv) {
+    if constexpr (XT_ONLY) {
+        const int bat = blockIdx.y;
+        uint4* xt = reinterpret_cast<uint4*>(a.xt + bat * a.np * a.mp) + int64_t(blockIdx.x) * 1024 + threadIdx.x;
+        const float sc = inv[bat];
+        uint4 w[4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) w[p] = xt[256 * p];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) xt[256 * p] = scale_bf16x8(w[p], sc);
+        return;
+    }
     __shared__ uint4 tileT[64][16];
     const int tid = threadIdx.x, bat = blockIdx.y;
     const int64_t q = blockIdx.x;
@@ -291,7 +312,7 @@ __global__ __launch_bounds__(256) void muon_scale_kernel(const PrepArgs a, const
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
         v[p] = scale_bf16x8(v[p], s);
-        if (a.scale_x) *reinterpret_cast<uint4*>(X + xoff(a.xkb, a.mp, a.np, i0 + 4 * rq + p, j0 + cg * 8)) = v[p];
+        *reinterpret_cast<uint4*>(X + xoff(a.xkb, a.mp, a.np, i0 + 4 * rq + p, j0 + cg * 8)) = v[p];
     }
     uint2* t2 = reinterpret_cast<uint2*>(&tileT[0][0]);
 #pragma unroll
@@ -1447,18 +1468,20 @@ int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double we
     pa.w_nest = float(beta);
     // Workspace matrices k-blocked whenever a whole matrix's byte offsets fit the
     // 31-bit buffer offsets.
-    pa.xkb = (p.mp * p.np * 2 < (int64_t(1) << 31)) ? 1 : 0;
-    // k-blocked: the Gram reads X^T k-major, so X is needed by nothing after
-    // the scale kernel and the updates write X^T only.  Row-major (matrices
-    // too large for 31-bit offsets): the Gram reads X, which every update
-    // writes beside X^T.
+    pa.xkb = p.xkb;
+    // k-blocked: the Gram reads X^T k-major, so X is needed by nothing: prep
+    // writes X^T, the scale pass rescales it in place and the updates write
+    // X^T only.  Row-major (matrices too large for 31-bit offsets): the Gram
+    // reads X, which prep writes, the scale pass rescales and transposes, and
+    // every update writes beside X^T.
     const bool kmajor = pa.xkb != 0;
-    pa.scale_x = kmajor ? 0 : 1;
+    pa.xt_direct = kmajor ? 1 : 0;
+    if (kmajor) pa.x = nullptr;  // no X in a k-blocked workspace
     pa.grad_scale = grad_scale;
     pa.found_inf = found_inf;
     const double B = double(batch), m = double(p.m), n = double(p.n);
     dim3 pgrid(unsigned(p.prep_tiles / 2), unsigned(batch));  // two prep units per block
-    // prep: read grad, momentum; write momentum, X (4 + 4 + 4 + 2 bytes per element)
+    // prep: read grad, momentum; write momentum, X^T or X (4 + 4 + 4 + 2 bytes per element)
     const double prep_bytes = 14.0 * B * m * n;
     hipError_t e = nesterov ? launch(K_MUON_PREP, 1, 0.0, prep_bytes, muon_prep_kernel<true>, pgrid, dim3(256), s,
                                      descs, pa)
@@ -1468,10 +1491,17 @@ int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double we
     e = launch(K_MUON_NORM, 0, 0.0, 4.0 * B * double(p.prep_tiles), muon_norm_kernel, dim3(unsigned(batch)),
                dim3(256), s, static_cast<const float*>(part), p.prep_tiles, eps, inv);
     if (e != hipSuccess) return int(e);
-    // scale: read X; write XT (and X) (2 + 2 (+ 2) bytes per padded element), two prep units per block
-    const dim3 sgrid(unsigned(p.prep_tiles / 2), unsigned(batch));
-    e = launch(K_MUON_SCALE, 0, 0.0, (kmajor ? 4.0 : 6.0) * B * double(p.mp) * double(p.np), muon_scale_kernel,
-               sgrid, dim3(256), s, pa, static_cast<const float*>(inv));
+    // scale: read X^T, write X^T (2 + 2 bytes per padded element; mp and np are
+    // multiples of 128, so 8192 elements per block divide each matrix); or
+    // read X, write X and X^T (2 + 2 + 2 bytes), two prep units per block
+    if (kmajor)
+        e = launch(K_MUON_SCALE, 1, 0.0, 4.0 * B * double(p.mp) * double(p.np), muon_scale_kernel<true>,
+                   dim3(unsigned(p.mp * p.np / 8192), unsigned(batch)), dim3(256), s, pa,
+                   static_cast<const float*>(inv));
+    else
+        e = launch(K_MUON_SCALE, 0, 0.0, 6.0 * B * double(p.mp) * double(p.np), muon_scale_kernel<false>,
+                   dim3(unsigned(p.prep_tiles / 2), unsigned(batch)), dim3(256), s, pa,
+                   static_cast<const float*>(inv));
     if (e != hipSuccess) return int(e);
 
     if (ns_steps == 0) {
