@@ -205,35 +205,44 @@ def group_sizes(count: int, cap: int, m: int, n: int, cus: int) -> list[int]:
     (``m = min(R, C)``, ``n = max(R, C)``), each at most ``cap``.
 
     Every group runs its Gram, polynomial and update GEMMs as one grid each,
-    and a grid whose workgroups do not fill whole rounds of the GPU's
-    ``cus`` compute units leaves CUs idle in its last round.  The cost of a
-    group of k matrices is modelled as the rounds of each product times its
-    reduction length (Gram: n, polynomial and update: m), plus a quarter
-    round of each per group for its launches; among splits into g near-equal
-    groups for g from ceil(count / cap) up, the cheapest wins (ties: fewer
-    groups).  Tiles follow the library's choice (256 x 256 from m = 2048,
-    one workgroup per CU; else 128 x 128, two per CU).
+    and a grid whose workgroups do not fill whole rounds of the GPU's CU slots
+    leaves CUs idle in its last round.  The cost of a group of k matrices is
+    modelled as each product's rounds times its reduction length (Gram: n,
+    polynomial and update: m) times the relative time of one k step of its
+    tile (a 256 x 256 step, one workgroup per CU, counts 1.4 steps of the
+    128 x 128 tile, two workgroups per CU), plus a quarter round of each
+    product per group for its launches.  The cheapest split into groups of any
+    sizes wins (ties: fewer groups), found by dynamic programming over the
+    number of matrices covered.  Tiles follow the library's choice: 256 x 256
+    from m = 2048, else 128 x 128, and the updates 256 x 256 from m = 1024
+    when both padded edges are multiples of 256.
     """
     if count <= 0:
         return []
     cap = max(1, min(cap, count))
     tile = 256 if m >= 2048 else 128
-    slots = cus * (1 if tile == 256 else 2)
-    tm, tn = -(-m // tile), -(-n // tile)
-    sym, full = tm * (tm + 1) // 2, tm * tn
+    mp, np_ = -(-m // tile) * tile, -(-n // tile) * tile
+    utile = 256 if (tile == 128 and m >= 1024 and mp % 256 == 0 and np_ % 256 == 0) else tile
+    step = {128: 1.0, 256: 1.4}
+    tm = mp // tile
+    sym = tm * (tm + 1) // 2
+    upd = (mp // utile) * (np_ // utile)
 
     def cost(k: int) -> float:
-        rounds = lambda tiles: -(-tiles * k // slots)  # noqa: E731
-        return rounds(sym) * (n + m) + rounds(full) * m + 0.25 * (n + 2 * m)
+        rounds = lambda tiles, t: -(-tiles * k // (cus * (1 if t == 256 else 2)))  # noqa: E731
+        return (rounds(sym, tile) * step[tile] * (n + m) + rounds(upd, utile) * step[utile] * m
+                + 0.25 * (step[tile] * (n + m) + step[utile] * m))
 
-    best = None
-    g_min = -(-count // cap)
-    for g in range(g_min, min(count, g_min + 4) + 1):
-        sizes = [count // g + (1 if i < count % g else 0) for i in range(g)]
-        c = sum(cost(k) for k in sizes)
-        if best is None or c < best[0] - 1e-9:
-            best = (c, sizes)
-    return best[1]
+    # best[c]: (cost, number of groups, sizes) of the cheapest split of c matrices
+    best: list = [(0.0, 0, [])] + [None] * count
+    for c in range(1, count + 1):
+        for k in range(1, min(cap, c) + 1):
+            pc, pg, ps = best[c - k]
+            cand = (pc + cost(k), pg + 1, ps + [k])
+            cur = best[c]
+            if cur is None or cand[0] < cur[0] - 1e-9 or (abs(cand[0] - cur[0]) <= 1e-9 and cand[1] < cur[1]):
+                best[c] = cand
+    return sorted(best[count][2], reverse=True)
 
 
 class _Call:
