@@ -272,7 +272,9 @@ __global__ __launch_bounds__(256) void muon_norm_kernel(const float* __restrict_
 
 // XT_ONLY (xt_direct): XT = bf16(XT * inv[b]) in place, a plain stream of
 // 16-byte pieces, four per thread (all loads before the stores), 8192
-// elements per block.
+// elements per block; NT: non-temporal loads and stores (for a group's X^T
+// larger than the memory-side cache: 8% faster there, 15% slower on groups it
+// holds).
 // Otherwise (the row-major workspace): XT = bf16(X * inv[b])^T and
 // X <- bf16(X * inv[b]) in place, one 128 x 64 tile of X per block (two prep
 // units), 16-byte global accesses throughout.  Each thread scales a 4 x 8
@@ -284,17 +286,28 @@ __global__ __launch_bounds__(256) void muon_norm_kernel(const float* __restrict_
 // kernel's LDS cycles in bank conflicts).
 __device__ __forceinline__ int scale_swz(int c) { return ((c >> 3) << 1) ^ (c & 3); }
 
-template <bool XT_ONLY>
+template <bool XT_ONLY, bool NT = false>
 __global__ __launch_bounds__(256) void muon_scale_kernel(const PrepArgs a, const float* __restrict__ inv) {
     if constexpr (XT_ONLY) {
         const int bat = blockIdx.y;
         uint4* xt = reinterpret_cast<uint4*>(a.xt + bat * a.np * a.mp) + int64_t(blockIdx.x) * 1024 + threadIdx.x;
         const float sc = inv[bat];
+        typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
         uint4 w[4];
+        if constexpr (NT) {
 #pragma unroll
-        for (int p = 0; p < 4; ++p) w[p] = xt[256 * p];
+            for (int p = 0; p < 4; ++p)
+                w[p] = __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(xt + 256 * p)));
 #pragma unroll
-        for (int p = 0; p < 4; ++p) xt[256 * p] = scale_bf16x8(w[p], sc);
+            for (int p = 0; p < 4; ++p)
+                __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, scale_bf16x8(w[p], sc)),
+                                            reinterpret_cast<u32x4_t*>(xt + 256 * p));
+        } else {
+#pragma unroll
+            for (int p = 0; p < 4; ++p) w[p] = xt[256 * p];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) xt[256 * p] = scale_bf16x8(w[p], sc);
+        }
         return;
     }
     __shared__ uint4 tileT[64][16];
@@ -1494,8 +1507,12 @@ int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double we
     // scale: read X^T, write X^T (2 + 2 bytes per padded element; mp and np are
     // multiples of 128, so 8192 elements per block divide each matrix); or
     // read X, write X and X^T (2 + 2 + 2 bytes), two prep units per block
+    // Non-temporal in-place scaling once the group's X^T exceeds the 256 MiB
+    // memory-side cache.
+    const bool scale_nt = B * double(p.mp) * double(p.np) * 2.0 > double(256u << 20);
     if (kmajor)
-        e = launch(K_MUON_SCALE, 1, 0.0, 4.0 * B * double(p.mp) * double(p.np), muon_scale_kernel<true>,
+        e = launch(K_MUON_SCALE, scale_nt ? 3 : 1, 0.0, 4.0 * B * double(p.mp) * double(p.np),
+                   scale_nt ? muon_scale_kernel<true, true> : muon_scale_kernel<true, false>,
                    dim3(unsigned(p.mp * p.np / 8192), unsigned(batch)), dim3(256), s, pa,
                    static_cast<const float*>(inv));
     else
