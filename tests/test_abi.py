@@ -171,8 +171,19 @@ def _rup(x, t):
     return (x + t - 1) // t * t
 
 
+def _tile(batch, m, n):
+    """The documented tile rule: 256 from m = 2048; from m = 1024 for batches
+    of 8 or more when the 256 padding adds at most 1/16 to the 128 padding."""
+    if m >= 2048:
+        return 256
+    if m >= 1024 and batch >= 8 and _rup(m, 256) * _rup(n, 256) * 16 <= _rup(m, 128) * _rup(n, 128) * 17:
+        return 256
+    return 128
+
+
 @pytest.mark.parametrize("batch,rows,cols,steps", [(1, 768, 3072, 5), (24, 3072, 768, 5), (16, 14336, 4096, 5),
-                                                   (3, 100, 37, 1), (2, 5, 7, 0), (1, 32768, 32768, 5)])
+                                                   (3, 100, 37, 1), (2, 5, 7, 0), (1, 32768, 32768, 5),
+                                                   (16, 1024, 2100, 5), (4, 1024, 2100, 5), (16, 1100, 4096, 5)])
 def test_workspace_layout(batch, rows, cols, steps):
     """X (bf16, mp x np per matrix) is kept only in a row-major workspace (a
     matrix of 2^31 bytes or more); then X^T twice, A and B, the prep partial
@@ -180,7 +191,7 @@ def test_workspace_layout(batch, rows, cols, steps):
     st, got = _ws(batch, rows, cols, steps)
     assert st == OK
     m, n = min(rows, cols), max(rows, cols)
-    tile = 256 if m >= 2048 else 128
+    tile = _tile(batch, m, n)
     mp, np_ = _rup(m, tile), _rup(n, tile)
     a = lambda x: _rup(x, 256)  # noqa: E731
     xe = batch * mp * np_ * 2

@@ -231,16 +231,20 @@ def test_capturable_flag():
 def _brute_cost(sizes, m, n, cus):
     """Modelled time of a split, counted tile by tile: each product's rounds of
     CU slots times its reduction length times the relative k-step time of its
-    tile (256 x 256 updates from m = 1024 when the padded edges allow), plus a
-    quarter round of each product per group."""
-    tile = 256 if m >= 2048 else 128
-    mp, np_ = -(-m // tile) * tile, -(-n // tile) * tile
-    utile = 256 if (tile == 128 and m >= 1024 and mp % 256 == 0 and np_ % 256 == 0) else tile
+    tile (the group's tile: 256 from m = 2048, or from m = 1024 for groups of 8
+    or more when the padding allows; on the 128 tile, 256-wide updates from
+    m = 1024 when the padded edges allow), plus a quarter round of each
+    product per group."""
     w = {128: 1.0, 256: 1.4}
     slots = {128: 2 * cus, 256: cus}
-    tm = mp // tile
+    rup = lambda x, t: -(-x // t) * t  # noqa: E731
     total = 0.0
     for k in sizes:
+        tile = 256 if m >= 2048 or (m >= 1024 and k >= 8 and rup(m, 256) * rup(n, 256) * 16
+                                    <= rup(m, 128) * rup(n, 128) * 17) else 128
+        mp, np_ = rup(m, tile), rup(n, tile)
+        utile = 256 if (tile == 128 and m >= 1024 and mp % 256 == 0 and np_ % 256 == 0) else tile
+        tm = mp // tile
         sym = sum(1 for i in range(tm) for j in range(tm) if j >= i) * k
         full = sum(1 for i in range(mp // utile) for j in range(np_ // utile)) * k
         total += math.ceil(sym / slots[tile]) * w[tile] * (n + m) + math.ceil(full / slots[utile]) * w[utile] * m
@@ -286,11 +290,12 @@ def test_launch_group_sizes_llama():
     """The Llama-3-8B classes: groups of 32 where the 136 symmetric tiles of a
     4096-row Gram fill whole rounds of 256 CUs (17 rounds for 32 matrices,
     where 20 matrices take 11 rounds for 62.5% of the work); the 64 k/v
-    (1024 x 4096) matrices as 28 + 28 + 8, whose 128-wide Gram and polynomial
-    grids (36 tiles per matrix, two workgroups per CU) fill 2 + 2 + 1 rounds
-    instead of 3 + 3 (measured 6.41 against 6.69 ms for the class's step)."""
+    (1024 x 4096) matrices as 24 + 24 + 16 on 256-wide tiles (10 symmetric
+    tiles per matrix: one round per group; updates 6 + 6 + 4 whole rounds;
+    measured 5.76 ms for the class's step against 6.17 ms as 28 + 28 + 8 on
+    the 128 tile)."""
     from triton_muon_adamw.muon.hip_muon import group_sizes
     assert group_sizes(96, 32, 4096, 14336, 256) == [32, 32, 32]
     assert group_sizes(64, 32, 4096, 4096, 256) == [32, 32]
-    assert group_sizes(64, 32, 1024, 4096, 256) == [28, 28, 8]
+    assert group_sizes(64, 32, 1024, 4096, 256) == [24, 24, 16]
     assert group_sizes(0, 32, 4096, 4096, 256) == []

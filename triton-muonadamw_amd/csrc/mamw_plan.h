@@ -91,7 +91,7 @@ struct MuonPlan {
     size_t bytes;
 };
 
-int choose_tile(int64_t m, int batch);
+int choose_tile(int64_t m, int64_t n, int batch);
 int muon_plan(int batch, int64_t rows, int64_t cols, int ns_steps, MuonPlan* plan);
 int muon_validate(const mamw_muon_matrix* mats, int batch, int ns_steps,
                   const void* workspace, size_t workspace_bytes, MuonPlan* plan,

@@ -1661,7 +1661,7 @@ extern "C" int mamw_ns_gram(const uint16_t* X, uint16_t* A, int batch, int64_t m
     if (!X || !A) return MAMW_ERR_NULL;
     if (!al16(X) || !al16(A)) return MAMW_ERR_ALIGN;
     if (ranges_overlap(X, bf16_bytes(batch, m, k), A, bf16_bytes(batch, m, m))) return MAMW_ERR_ALIAS;
-    const int tile = (m % 256 == 0) ? choose_tile(m, batch) : 128;
+    const int tile = (m % 256 == 0) ? choose_tile(m, k, batch) : 128;
     MuonBatchDescs d{};
     return int(launch_gemm<MODE_GRAM>(tile, gram_args(X, A, m, k, tile), d, batch,
                                       double(batch) * double(m) * double(m) * double(k),
@@ -1675,7 +1675,7 @@ extern "C" int mamw_ns_poly(const uint16_t* A, uint16_t* B, int batch, int64_t m
     if (!A || !B) return MAMW_ERR_NULL;
     if (!al16(A) || !al16(B)) return MAMW_ERR_ALIGN;
     if (ranges_overlap(A, bf16_bytes(batch, m, m), B, bf16_bytes(batch, m, m))) return MAMW_ERR_ALIAS;
-    const int tile = (m % 256 == 0) ? choose_tile(m, batch) : 128;
+    const int tile = (m % 256 == 0) ? choose_tile(m, m, batch) : 128;
     MuonBatchDescs d{};
     return int(launch_gemm<MODE_POLY>(tile, poly_args(A, B, m, tile, b, c), d, batch,
                                       double(batch) * double(m) * double(m) * double(m),
@@ -1699,7 +1699,7 @@ extern "C" int mamw_ns_update(const uint16_t* B, const uint16_t* X, const uint16
                   ranges_overlap(out_t, xb, out, xb)))
         return MAMW_ERR_ALIAS;
     (void)X;  // X enters through its transpose XT (operand and epilogue source)
-    const int tile = (m % 256 == 0 && n % 256 == 0) ? choose_tile(m, batch) : 128;
+    const int tile = (m % 256 == 0 && n % 256 == 0) ? choose_tile(m, n, batch) : 128;
     MuonBatchDescs d{};
     return int(launch_gemm<MODE_UPDATE>(tile, update_args(B, XT, out, out_t, m, n, tile, a), d, batch,
                                         2.0 * double(batch) * double(m) * double(m) * double(n),

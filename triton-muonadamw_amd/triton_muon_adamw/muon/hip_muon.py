@@ -200,6 +200,18 @@ def muon_step(weights: torch.Tensor, grad: torch.Tensor, momentum: torch.Tensor,
     _lib.check(st, "mamw_muon_step")
 
 
+def gemm_tile(m: int, n: int, batch: int) -> int:
+    """The library's GEMM tile edge for a launch group (``mamw_plan.cpp``
+    ``choose_tile``): 256 from m = 2048; from m = 1024 for batches of 8 or
+    more when the 256 padding adds at most 1/16 to the 128 padding; else 128."""
+    if m >= 2048:
+        return 256
+    rup = lambda x, t: -(-x // t) * t  # noqa: E731
+    if m >= 1024 and batch >= 8 and rup(m, 256) * rup(n, 256) * 16 <= rup(m, 128) * rup(n, 128) * 17:
+        return 256
+    return 128
+
+
 def group_sizes(count: int, cap: int, m: int, n: int, cus: int) -> list[int]:
     """Sizes of the launch groups for ``count`` matrices of one shape class
     (``m = min(R, C)``, ``n = max(R, C)``), each at most ``cap``.
@@ -213,22 +225,21 @@ def group_sizes(count: int, cap: int, m: int, n: int, cus: int) -> list[int]:
     128 x 128 tile, two workgroups per CU), plus a quarter round of each
     product per group for its launches.  The cheapest split into groups of any
     sizes wins (ties: fewer groups), found by dynamic programming over the
-    number of matrices covered.  Tiles follow the library's choice: 256 x 256
-    from m = 2048, else 128 x 128, and the updates 256 x 256 from m = 1024
-    when both padded edges are multiples of 256.
+    number of matrices covered.  Tiles follow the library's choice for the
+    group's size (``gemm_tile``), and a group on the 128 tile takes 256 x 256
+    updates from m = 1024 when both padded edges are multiples of 256.
     """
     if count <= 0:
         return []
     cap = max(1, min(cap, count))
-    tile = 256 if m >= 2048 else 128
-    mp, np_ = -(-m // tile) * tile, -(-n // tile) * tile
-    utile = 256 if (tile == 128 and m >= 1024 and mp % 256 == 0 and np_ % 256 == 0) else tile
     step = {128: 1.0, 256: 1.4}
-    tm = mp // tile
-    sym = tm * (tm + 1) // 2
-    upd = (mp // utile) * (np_ // utile)
 
     def cost(k: int) -> float:
+        tile = gemm_tile(m, n, k)
+        mp, np_ = -(-m // tile) * tile, -(-n // tile) * tile
+        utile = 256 if (tile == 128 and m >= 1024 and mp % 256 == 0 and np_ % 256 == 0) else tile
+        tm = mp // tile
+        sym, upd = tm * (tm + 1) // 2, (mp // utile) * (np_ // utile)
         rounds = lambda tiles, t: -(-tiles * k // (cus * (1 if t == 256 else 2)))  # noqa: E731
         return (rounds(sym, tile) * step[tile] * (n + m) + rounds(upd, utile) * step[utile] * m
                 + 0.25 * (step[tile] * (n + m) + step[utile] * m))
