@@ -69,8 +69,10 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // ---------------------------------------------------------------------------
 // Prep: one tile of 64 x 128 parameter elements per block, two prep units
 // of 32 rows (parameter rows read in 512-byte runs; 64 x 64 tiles measured 6%
-// slower).  A wide matrix writes it as a 64 x 128 tile of X; a tall one
-// transposes it through LDS into 128 full 128-byte rows of X.
+// slower).  The output is X^T (k-blocked workspace) or X (row-major): where
+// parameter rows are output rows (X^T of a tall matrix, X of a wide one) the
+// tile is written as it stands, otherwise it is transposed through LDS into
+// 128 full 128-byte output rows.
 
 struct PrepArgs {
     uint16_t* x;    // [batch][mp][np], k-blocked when xkb (see xoff)
