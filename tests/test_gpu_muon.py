@@ -171,6 +171,45 @@ def test_batched_equals_single(gpu):
         assert torch.equal(a.detach(), b.detach())
 
 
+def test_tile_edge_does_not_change_the_bits(gpu):
+    """Eight 1024 x 2048 matrices in one launch group run on 256-wide tiles
+    (m >= 1024 and 8 matrices) with lower-triangle A and B; each alone runs
+    its Gram and polynomial on 128-wide tiles with mirrored A and B (the
+    updates take 256-wide tiles from m = 1024 either way).  Every output
+    element sums the same products in the same order under either tile and
+    layout, so parameters and momenta agree bit for bit (two steps)."""
+    from triton_muon_adamw import _lib
+    shapes = [(1024, 2048)] * 8
+    ps, gs, ms, params, opt = _run_muon(shapes, gpu, seed=9)
+    singles = []
+    for p, g, m in zip(ps, gs, ms):
+        q = torch.nn.Parameter(p.to(gpu))
+        q.grad = g.to(gpu)
+        o = HipMuon([q], lr=opt.lr, coeffs=COEFFS)
+        o.momentum[q].copy_(m)
+        singles.append((q, o))
+
+    def tiles_of(step_fn):
+        _lib.prof_start()
+        step_fn()
+        _lib.prof_stop()
+        return {(r["kernel"].split(":")[1], r["variant"] // 8) for r in _lib.prof_collect()
+                if r["kernel"].startswith("ns_gemm")}
+
+    assert tiles_of(opt.step) == {("gram", 256), ("poly", 256), ("update", 256), ("apply", 256)}
+    assert [c.n for c in opt._calls] == [8]
+    # alone: 128-wide Gram and polynomial, 256-wide updates (m = 1024)
+    assert tiles_of(lambda: [o.step() for _, o in singles]) == {("gram", 128), ("poly", 128), ("update", 256),
+                                                                 ("apply", 256)}
+    opt.step()
+    for q, o in singles:
+        o.step()
+    torch.cuda.synchronize()
+    for a, (b, o) in zip(params, singles):
+        assert torch.equal(a.detach(), b.detach())
+        assert torch.equal(opt.momentum[a], o.momentum[b])
+
+
 @pytest.mark.parametrize("on_side_stream", [False, True])
 def test_concurrent_classes_equal_in_order(gpu, on_side_stream):
     """Shape classes on their own streams (small steps) give the same bits as one after another,
