@@ -241,6 +241,42 @@ def test_concurrent_classes_equal_in_order(gpu, on_side_stream):
         assert torch.equal(a, b)
 
 
+# Launch groups that exercise the tile and storage choices: two block rows
+# (m just above 128, lower-triangle A and B), ragged n, tall matrices, the
+# 256-wide tile from m = 1024 in groups of 8 or more (and the padding rule
+# that keeps the 128 tile), and m >= 2048.
+SWEEP = [(3, (200, 520)), (5, (700, 260)), (1, (129, 4000)), (8, (1024, 1300)), (9, (1100, 2100)),
+         (8, (1024, 2100)), (8, (1280, 2560)), (8, (4096, 1024)), (2, (2100, 2300))]
+
+
+@pytest.mark.parametrize("count,shape", SWEEP)
+def test_group_sweep_vs_torch(gpu, count, shape):
+    """A launch group of ``count`` matrices of ``shape``: every matrix's update
+    (recovered from the parameter change, in float64) against torch's
+    Newton-Schulz (``torch.optim._muon._zeropower_via_newtonschulz``) of the
+    same Nesterov blend, relative Frobenius error <= 1e-2."""
+    from torch.optim._muon import _zeropower_via_newtonschulz
+    from triton_muon_adamw.muon.hip_muon import gemm_tile
+    lr, wd = 2e-2, 0.1
+    ps, gs, ms, params, opt = _run_muon([shape] * count, gpu, seed=11, lr=lr, weight_decay=wd)
+    mom0 = [opt.momentum[p].clone() for p in params]
+    opt.step()
+    torch.cuda.synchronize()
+    assert [c.n for c in opt._calls] == [count]
+    m_, n_ = min(shape), max(shape)
+    assert gemm_tile(m_, n_, count) == (256 if m_ >= 2048 or shape in ((1024, 2100), (1280, 2560), (4096, 1024))
+                                        else 128)
+    keep = 1 - lr * wd
+    slr = scaled_lr(lr, "original", *shape)
+    for p0, p, g, m0 in zip(ps, params, gs, mom0):
+        g = g.to(gpu)
+        mom = m0.lerp(g, 1 - 0.95)
+        ref = _zeropower_via_newtonschulz(g.lerp(mom, 0.95), COEFFS, 5, 1e-7).double()
+        u = (p0.to(gpu).double() * keep - p.detach().double()) / slr
+        err = ((u - ref).norm() / ref.norm()).item()
+        assert err <= 1e-2, f"{count} x {shape}: update rel err {err} against torch's Newton-Schulz"
+
+
 @pytest.mark.parametrize("shape", [(768, 3072), (1024, 4096), (4096, 4096), (14336, 4096)])
 def test_config3_ns_vs_torch(gpu, shape):
     """Config 3 shapes: blend momentum (beta 0.95, Nesterov), NS in bf16 vs torch's routine on the GPU."""
