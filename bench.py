@@ -282,6 +282,42 @@ def bench_ns_c3(dev, steps, warmup):
             "mfma_frac_over_step": round(tf / PEAK_BF16_TFLOPS, 4), "ns_flops": flops}
 
 
+def bench_kv_class(dev, steps, warmup):
+    """The Llama-8B step's k/v shape class alone: 64 matrices of 1024 x 4096
+    (32 layers x k_proj, v_proj) through HipMuon, as the full step groups
+    them.  Reports the class's step time (prep, norm and scale included), the
+    Newton-Schulz GEMM time from a profiled pass, and both rates over the
+    symmetric-minimal NS work."""
+    import torch
+
+    from helpers import ns_flops
+    from triton_muon_adamw.muon import HipMuon
+
+    mc, _ = configs()
+    gen = torch.Generator(device=dev).manual_seed(2)
+    params = []
+    for _ in range(64):
+        p = torch.nn.Parameter(torch.empty((1024, 4096), device=dev).normal_(0.0, 0.02, generator=gen))
+        p.grad = torch.empty((1024, 4096), device=dev).normal_(0.0, 1e-3, generator=gen)
+        params.append(p)
+    opt = HipMuon(params, lr=mc.lr, weight_decay=mc.weight_decay, coeffs=mc.coeffs, nesterov=True, beta=0.95,
+                  ns_steps=5, eps=mc.eps)
+    ms, _, _ = time_steps(opt, steps, warmup)
+    _, _, recs = time_steps(opt, steps, 1, profile=True)
+    ns_ms = sum(r["ms"] for r in recs if r["kernel"].startswith("ns_gemm")) / steps
+    flops = 64 * ns_flops((1024, 4096))
+    groups = [c.n for c in opt._calls]
+    log(f"[kv class] 64 x 1024x4096 in groups {groups}: step {ms:.3f} ms, NS GEMMs {ns_ms:.3f} ms -> "
+        f"{flops / (ns_ms * 1e-3) / 1e12:.1f} TFLOP/s over the GEMMs")
+    del opt, params
+    torch.cuda.empty_cache()
+    return {"groups": groups, "step_ms": round(ms, 4), "ns_gemm_ms": round(ns_ms, 4), "ns_flops": flops,
+            "TFLOP/s_over_step": round(flops / (ms * 1e-3) / 1e12, 1),
+            "mfma_frac_over_step": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "TFLOP/s_over_gemms": round(flops / (ns_ms * 1e-3) / 1e12, 1),
+            "mfma_frac_over_gemms": round(flops / (ns_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+
+
 def llama_cpu_sample(named):
     """Host copies of the CPU baseline's sample, taken from the GPU run's own
     tensors before its first step: layer 0's seven Muon matrices and two
@@ -580,6 +616,7 @@ def main():
                                                for k, a in sorted(g_agg.items(), key=lambda kv: -kv[1]["ms"])}}
         extras["adamw_c2"] = bench_adamw_c2(dev, max(args.steps, 20), max(args.warmup, 3))
         extras["ns_c3"] = bench_ns_c3(dev, args.steps, args.warmup)
+        extras["llama_kv_class"] = bench_kv_class(dev, args.steps, args.warmup)
         extras["vs_torch_gpu"] = bench_vs_torch_gpu(dev, args.seed)
     cpu = None
     if not args.no_cpu:
