@@ -89,6 +89,19 @@ def test_checker_is_conservative_with_scalar_loads_and_branches():
     assert len(_asmcheck.check(_asm(fwd)).hazards) == 1
 
 
+def test_checker_follows_unconditional_branches():
+    # The block after an unconditional branch is reached only through its label: a use there is
+    # judged with the state of the branches that reach it, not the state before the branch.
+    skip = (READ.format(10, 11) + "\ts_branch .LBB0_3\n.LBB0_2:\n\tv_mov_b32 v10, 0\n\ts_endpgm\n"
+            ".LBB0_3:\n\ts_waitcnt lgkmcnt(0)\n\ts_cbranch_scc1 .LBB0_2\n")
+    assert _asmcheck.check(_asm(skip)).hazards == []
+    # ... and a block placed after s_endpgm that a branch reaches before the wait is still checked.
+    late = (READ.format(10, 11) + "\ts_cbranch_scc1 .LBB0_2\n\ts_waitcnt lgkmcnt(0)\n\ts_endpgm\n"
+            ".LBB0_2:\n\tv_mov_b32 v20, v11\n\ts_waitcnt lgkmcnt(0)\n")
+    rep = _asmcheck.check(_asm(late))
+    assert len(rep.hazards) == 1 and "v11" in rep.hazards[0]
+
+
 PROBE = r"""
 #include <hip/hip_runtime.h>
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));

@@ -297,3 +297,74 @@ def test_config3_ns_vs_torch(gpu, shape):
     torch.testing.assert_close(m, m_ref, atol=0, rtol=2.4e-7)  # lerp with one fma: <= 2 ulp of torch's
     err = (out - ref).norm().item() / ref.norm().item()
     assert err <= 1e-2, f"{shape}: NS rel err vs torch {err}"
+
+
+
+def _orthogonal_signs(rows, cols, rng):
+    """rows x cols, rows mutually orthogonal: distinct rows of the Sylvester
+    Hadamard matrix of order 4096 (entry (-1)^popcount(i & j)), with random
+    column signs, placed on 4096 random columns (zero elsewhere)."""
+    r = rng.choice(4096, size=rows, replace=False)
+    x = np.bitwise_and.outer(r, np.arange(4096))
+    pop = np.zeros_like(x)
+    while x.any():
+        pop += x & 1
+        x >>= 1
+    h = np.where(pop & 1, -1.0, 1.0).astype(np.float32) * rng.choice([-1.0, 1.0], size=4096).astype(np.float32)
+    out = np.zeros((rows, cols), np.float32)
+    out[:, rng.permutation(cols)[:4096]] = h
+    return out
+
+
+
+@pytest.mark.parametrize("count,shape", [(16, (1024, 4096)), (1, (14336, 4096))])
+def test_ns_exact_on_orthogonal_rows(gpu, count, shape):
+    """The whole Newton-Schulz pipeline on inputs where every product is exact
+    in any summation order, so the result is known bit for bit.
+
+    The gradients' rows (in the m x n orientation) are orthogonal +-1 vectors
+    with 4096 nonzeros; with zero momentum, beta = 0 and no Nesterov blend,
+    X0 = G / ||G||_F = +-2^-e exactly (||G||_F = 2^e), every Gram partial sum
+    is an integer multiple of 2^-2e below 2^24 of them, and A = X0 X0^T =
+    lam I with lam = 4096 * 2^-2e.  Coefficients (0, 1/lam, 0) make B = I and
+    every iterate X0 again, so with zero parameters the step writes
+    -slr * X0 = -s G for one scalar s = slr * 2^-e.  A k block lost, doubled
+    or summed into another tile, a block of A or B above the diagonal read
+    from the wrong place, or an iterate tile written to the wrong place moves
+    A off lam I or the iterates off X0 (a lost 64-column block moves 80-90% of
+    an off-diagonal tile of A).  The 16 matrices of 1024 x 4096 run on
+    256-wide tiles with lower-triangle A and B; each stepped alone (128-wide
+    Gram and polynomial, mirrored A and B) gives the same bits.  The
+    14336 x 4096 matrix runs transposed."""
+    rng = np.random.default_rng(17)
+    m_, n_ = min(shape), max(shape)
+    grads = []
+    for _ in range(count):
+        x = _orthogonal_signs(m_, n_, rng)
+        grads.append(torch.from_numpy(x if shape[0] <= shape[1] else np.ascontiguousarray(x.T)))
+    e = (int(np.log2(m_)) + 12) // 2  # ||G||_F^2 = m * 4096
+    lam = 4096.0 * 2.0 ** (-2 * e)
+    coeffs = (0.0, 1.0 / lam, 0.0)
+    lr = 2e-2
+
+    def make(gs):
+        params = [torch.nn.Parameter(torch.zeros(shape, device=gpu)) for _ in gs]
+        for q, g in zip(params, gs):
+            q.grad = g.to(gpu)
+        return params, HipMuon(params, lr=lr, coeffs=coeffs, beta=0.0, nesterov=False, weight_decay=0.1)
+
+    params, opt = make(grads)
+    opt.step()
+    assert [c.n for c in opt._calls] == [count]
+    slr = scaled_lr(lr, "original", *shape)
+    for i, (q, g) in enumerate(zip(params, grads)):
+        got = q.detach().cpu()
+        s = got.abs().max().item()
+        assert torch.equal(got, -s * g), f"matrix {i}: not -s * G ({(got != -s * g).sum().item()} elements off)"
+        assert abs(s - slr * 2.0 ** -e) <= 1e-6 * slr * 2.0 ** -e, f"matrix {i}: {s}"
+    if count > 1:
+        singles = [make([g]) for g in grads]
+        for _, o in singles:
+            o.step()
+        for q, (qs, _) in zip(params, singles):
+            assert torch.equal(q.detach(), qs[0].detach())

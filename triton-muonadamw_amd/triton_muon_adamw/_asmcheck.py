@@ -16,7 +16,10 @@ but the N youngest, or nothing for N > 0 while a scalar memory load (which
 completes out of order) is outstanding.  The scan follows the code in order;
 at a forward branch the outstanding list is remembered and merged into the
 state at its target label, and a backward branch re-scans from its target
-with the branch's state until everything pending has been retired.
+with the branch's state until everything pending has been retired.  Nothing
+falls through an unconditional branch or ``s_endpgm``: the block after one is
+reached through its label only.  A kernel is scanned up to its
+``.Lfunc_end`` label, so blocks placed after ``s_endpgm`` are covered.
 """
 
 from __future__ import annotations
@@ -98,8 +101,12 @@ def _step(inst: _Inst, state: list[_Op], hazards: list[str]) -> list[_Op]:
     return state
 
 
-def _kernels(asm: str, name_filter: str):
-    """Yield (kernel name, instructions, label -> index) for each kernel body."""
+def _kernels(asm: str, name_filter):
+    """Yield (kernel name, instructions, label -> index) for each kernel body:
+    everything from the kernel's symbol to its ``.Lfunc_end`` label, so the
+    blocks the compiler places after ``s_endpgm`` (reached only by branches)
+    are scanned too."""
+    names = (name_filter,) if isinstance(name_filter, str) else tuple(name_filter)
     cur, insts, labels, in_asm = None, [], {}, False
     for no, raw in enumerate(asm.splitlines(), 1):
         line = raw.strip()
@@ -107,10 +114,14 @@ def _kernels(asm: str, name_filter: str):
         if m and raw[0] not in " \t" and m.group(1).startswith("_Z"):
             if cur is not None:
                 yield cur, insts, labels
-            cur = m.group(1) if name_filter in m.group(1) else None
+            cur = m.group(1) if any(n in m.group(1) for n in names) else None
             insts, labels, in_asm = [], {}, False
             continue
         if cur is None:
+            continue
+        if m and m.group(1).startswith(".Lfunc_end"):
+            yield cur, insts, labels
+            cur = None
             continue
         if line.startswith(";;#ASMSTART"):
             in_asm = True
@@ -125,15 +136,13 @@ def _kernels(asm: str, name_filter: str):
         if not code or code.startswith("."):
             continue
         insts.append(_Inst(no, code, in_asm))
-        if code.startswith("s_endpgm"):
-            yield cur, insts, labels
-            cur = None
     if cur is not None:
         yield cur, insts, labels
 
 
-def check(asm: str, name_filter: str = "ns_gemm_kernel") -> Report:
-    """Scan every kernel whose mangled name contains ``name_filter``."""
+def check(asm: str, name_filter=("ns_gemm_kernel",)) -> Report:
+    """Scan every kernel whose mangled name contains ``name_filter`` (a
+    string or a tuple of them)."""
     rep = Report()
     for name, insts, labels in _kernels(asm, name_filter):
         hazards: list[str] = []
@@ -157,7 +166,11 @@ def check(asm: str, name_filter: str = "ns_gemm_kernel") -> Report:
                         s2 = _step(insts[j], s2, hazards)
                         if not any(op.kind == "asm" for op in s2):
                             break
-            if inst.text.startswith("s_endpgm") and any(op.kind == "asm" for op in state):
-                hazards.append(f"line {inst.line}: kernel ends with untracked reads in flight")
+            if inst.text.startswith("s_endpgm"):
+                if any(op.kind == "asm" for op in state):
+                    hazards.append(f"line {inst.line}: kernel ends with untracked reads in flight")
+                state = []  # nothing falls through: the next block is reached by branches only
+            elif b and inst.text.startswith("s_branch"):
+                state = []  # unconditional: the next block is reached by branches only
         rep.hazards += [f"{name}: {h}" for h in dict.fromkeys(hazards)]
     return rep
