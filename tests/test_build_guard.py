@@ -102,6 +102,29 @@ def test_checker_follows_unconditional_branches():
     assert len(rep.hazards) == 1 and "v11" in rep.hazards[0]
 
 
+def test_checker_follows_every_path_around_a_loop():
+    # The back edge reaches the use through a branch that skips the wait.
+    loop = (".LBB0_1:\n\ts_cbranch_scc1 .LBB0_2\n\ts_waitcnt lgkmcnt(0)\n.LBB0_2:\n\tv_mov_b32 v20, v10\n"
+            + READ.format(10, 11) + "\ts_cbranch_scc0 .LBB0_1\n\ts_waitcnt lgkmcnt(0)\n")
+    rep = _asmcheck.check(_asm(loop))
+    assert any("v10" in h and "v_mov_b32 v20, v10" in h for h in rep.hazards), rep.hazards
+    # With the wait on both paths the same loop is clean.
+    safe = loop.replace("\ts_cbranch_scc1 .LBB0_2\n", "")
+    assert _asmcheck.check(_asm(safe)).hazards == []
+    # A loop that issues reads into fresh registers and never waits inside
+    # settles (its outstanding list becomes a set) and is caught at the end.
+    grow = ".LBB0_1:\n" + READ.format(10, 11) + "\ts_cbranch_scc0 .LBB0_1\n"
+    rep = _asmcheck.check(_asm(grow))
+    assert any("ends with untracked reads in flight" in h for h in rep.hazards), rep.hazards
+
+
+def test_checker_rejects_unknown_control_flow():
+    rep = _asmcheck.check(_asm("\ts_cbranch_scc1 .LBB9_9\n"))
+    assert any("unknown label" in h for h in rep.hazards)
+    rep = _asmcheck.check(_asm("\ts_setpc_b64 s[0:1]\n"))
+    assert any("indirect transfer" in h for h in rep.hazards)
+
+
 PROBE = r"""
 #include <hip/hip_runtime.h>
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
