@@ -183,11 +183,14 @@ def _tile(batch, m, n):
 
 @pytest.mark.parametrize("batch,rows,cols,steps", [(1, 768, 3072, 5), (24, 3072, 768, 5), (16, 14336, 4096, 5),
                                                    (3, 100, 37, 1), (2, 5, 7, 0), (1, 32768, 32768, 5),
-                                                   (16, 1024, 2100, 5), (4, 1024, 2100, 5), (16, 1100, 4096, 5)])
+                                                   (16, 1024, 2100, 5), (4, 1024, 2100, 5), (16, 1100, 4096, 5),
+                                                   (1, 8192, 130816, 5), (1, 130816, 8192, 5), (1, 8192, 131072, 5)])
 def test_workspace_layout(batch, rows, cols, steps):
     """X (bf16, mp x np per matrix) is kept only in a row-major workspace (a
     matrix of 2^31 bytes or more); then X^T twice, A and B, the prep partial
-    sums and the norms, each region 256-byte aligned."""
+    sums and the norms, each region 256-byte aligned.  8192 x 130816 is the
+    largest k-blocked matrix of its row count (2^31 - 2^22 bytes); 8192 x
+    131072 is row-major."""
     st, got = _ws(batch, rows, cols, steps)
     assert st == OK
     m, n = min(rows, cols), max(rows, cols)

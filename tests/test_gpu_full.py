@@ -140,6 +140,17 @@ def test_llama8b_full_step_properties(gpu):
         del u, ref, mom, blend
 
 
+@pytest.mark.parametrize("shape", [(8192, 130816), (130816, 8192)])
+def test_largest_kblocked_matrix_vs_torch(gpu, shape):
+    """The largest k-blocked matrix with 8192 rows: its padded X^T is
+    2^31 - 2^22 bytes, so every byte offset inside a workspace matrix (the
+    32-bit buffer offsets of the GEMMs' loads and stores) comes within 4 MB of
+    2^31.  Every GEMM launch must be a k-blocked variant, and the update must
+    match torch's Newton-Schulz on the same Nesterov blend (relative Frobenius
+    error <= 1e-2, computed in row chunks); both orientations."""
+    _step_vs_torch(gpu, shape, kblocked=True)
+
+
 @pytest.mark.parametrize("shape", [(16384, 65536), (65536, 16384)])
 def test_rowmajor_workspace_path_vs_torch(gpu, shape):
     """A matrix whose padded size is 2^31 bf16 bytes: the workspace matrices
@@ -148,6 +159,12 @@ def test_rowmajor_workspace_path_vs_torch(gpu, shape):
     the step must be the row-major variant, and the update must match torch's
     Newton-Schulz on the same Nesterov blend (relative Frobenius error
     <= 1e-2, computed in row chunks)."""
+    _step_vs_torch(gpu, shape, kblocked=False)
+
+
+def _step_vs_torch(gpu, shape, kblocked):
+    """One Muon step of a single matrix: the GEMM variants' layout bit, then
+    the update against torch's Newton-Schulz in row chunks."""
     from triton_muon_adamw import _lib
     from triton_muon_adamw.muon import HipMuon
     gen = torch.Generator(device=gpu).manual_seed(11)
@@ -161,7 +178,7 @@ def test_rowmajor_workspace_path_vs_torch(gpu, shape):
     torch.cuda.synchronize()
     _lib.prof_stop()
     recs = [r for r in _lib.prof_collect() if r["kernel"].startswith("ns_gemm")]
-    assert len(recs) == 3 * MC.ns_steps and all(r["variant"] & 1 == 0 for r in recs), recs
+    assert len(recs) == 3 * MC.ns_steps and all(r["variant"] & 1 == int(kblocked) for r in recs), recs
     assert torch.isfinite(p).all()
     keep = 1 - MC.lr * MC.weight_decay
     adj = MC.lr * math.sqrt(max(1.0, shape[0] / shape[1]))
