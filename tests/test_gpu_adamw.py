@@ -51,6 +51,33 @@ def test_adamw_multi_tensor_bitexact_vs_oracle(gpu):
         assert np.array_equal(opt.v[p].cpu().numpy(), ref.v[i])
 
 
+def test_adamw_tensor_beyond_2pow31_elements(gpu):
+    """One tensor of 2^31 + 4097 elements (element offsets past 32 bits, a
+    ragged tail): one step, bit-exact against the oracle on three slices of
+    2^20 elements (the start, across element 2^31, and the end); the update
+    is elementwise, so each slice is checked on its own."""
+    n = (1 << 31) + 4097
+    gen = torch.Generator(device=gpu).manual_seed(13)
+    p = torch.nn.Parameter(torch.empty(n, device=gpu).normal_(0.0, 0.02, generator=gen))
+    p.grad = torch.empty(n, device=gpu).normal_(0.0, 1e-3, generator=gen)
+    opt = HipAdamW([p], **HP)
+    opt.m[p].normal_(0.0, 1e-4, generator=gen)
+    opt.v[p].normal_(0.0, 1e-6, generator=gen).abs_()
+    w = 1 << 20
+    cuts = [0, (1 << 31) - w // 2, n - w]
+    before = [[t[c:c + w].cpu().numpy() for t in (p.detach(), p.grad, opt.m[p], opt.v[p])] for c in cuts]
+    opt.step()
+    torch.cuda.synchronize()
+    b1, b2 = oracle.adamw.bias_corrections(*HP["betas"], 1)
+    for c, (p0, g0, m0, v0) in zip(cuts, before):
+        exp = oracle.adamw.adamw_update(p0, g0, m0, v0, lr=HP["lr"], bias1=b1, bias2=b2, beta1=HP["betas"][0],
+                                        beta2=HP["betas"][1], weight_decay=HP["weight_decay"], eps=HP["eps"])
+        for name, got, e in zip("pmv", (p.detach(), opt.m[p], opt.v[p]), exp):
+            assert np.array_equal(got[c:c + w].cpu().numpy(), e), f"{name}[{c}:{c + w}] differs from the oracle"
+    del p, opt
+    torch.cuda.empty_cache()
+
+
 def test_adamw_skips_none_grad_but_counts_step(gpu):
     p1 = torch.nn.Parameter(torch.randn(1000, device=gpu))
     p2 = torch.nn.Parameter(torch.randn(1000, device=gpu))
