@@ -151,6 +151,15 @@ def test_largest_kblocked_matrix_vs_torch(gpu, shape):
     _step_vs_torch(gpu, shape, kblocked=True)
 
 
+@pytest.mark.parametrize("shape", [(32768, 65600), (65600, 32768)])
+def test_matrix_beyond_2pow31_elements_vs_torch(gpu, shape):
+    """A parameter of 2,149,580,800 elements (element offsets past 32 bits in
+    prep, scale and the parameter writes of APPLY; 65600 columns leave ragged
+    tiles): row-major workspace, the update against torch's Newton-Schulz,
+    both orientations."""
+    _step_vs_torch(gpu, shape, kblocked=False)
+
+
 @pytest.mark.parametrize("shape", [(16384, 65536), (65536, 16384)])
 def test_rowmajor_workspace_path_vs_torch(gpu, shape):
     """A matrix whose padded size is 2^31 bf16 bytes: the workspace matrices
