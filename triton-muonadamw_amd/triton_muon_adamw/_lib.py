@@ -196,6 +196,42 @@ def stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+_HIP_STREAM_NON_BLOCKING = 1
+_side_streams: dict[int, list] = {}
+
+
+def side_streams(device: torch.device, count: int) -> list:
+    """``count`` streams of the library's own on ``device`` for shape classes
+    that run beside the caller's stream, made once per device and kept for the
+    life of the process.
+
+    They come from hipStreamCreateWithFlags(hipStreamNonBlocking), looked up
+    through this library's handle (so from the HIP runtime the library and
+    torch share), not from torch's stream pool: the runtime gives a new stream
+    the least used of its hardware queues (GPU_MAX_HW_QUEUES of them, 4 by
+    default), which keeps up to GPU_MAX_HW_QUEUES - 1 of these streams off the
+    queue of the null stream and off each other's.  Which queue a pool stream
+    shares depends on how many the pool has handed out before (measured: one
+    small Muon step 5.0 or 5.6 ms depending on that history).  Non-blocking:
+    the legacy null stream does not wait for them, nor they for it."""
+    idx = torch.device(device).index
+    if idx is None:
+        idx = torch.cuda.current_device()
+    have = _side_streams.setdefault(idx, [])
+    if len(have) < count:
+        create = load().hipStreamCreateWithFlags
+        create.restype = c_int
+        create.argtypes = [POINTER(c_void_p), ctypes.c_uint]
+        with torch.cuda.device(idx):
+            while len(have) < count:
+                s = c_void_p()
+                st = create(ctypes.byref(s), _HIP_STREAM_NON_BLOCKING)
+                if st != 0 or not s.value:
+                    raise RuntimeError(f"hipStreamCreateWithFlags failed on device {idx} (hipError {st})")
+                have.append(torch.cuda.ExternalStream(s.value, device=torch.device("cuda", idx)))
+    return have[:count]
+
+
 def prof_start() -> None:
     """Start timing every kernel launch of the library (HIP events per dispatch)."""
     check(load().mamw_prof_start(), "mamw_prof_start")

@@ -32,6 +32,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 from collections.abc import Iterable
 from typing import Literal
 
@@ -256,6 +257,35 @@ def group_sizes(count: int, cap: int, m: int, n: int, cus: int) -> list[int]:
     return sorted(best[count][2], reverse=True)
 
 
+def _class_flops(calls, key) -> float:
+    return sum(c.n * (3.0 * c.m * c.m * c.n_ + float(c.m) ** 3) for c in calls if (c.device, c.group) == key)
+
+
+def _lanes(calls) -> dict:
+    """Streams of concurrent shape classes, per device: the class with the
+    most Newton-Schulz work on the caller's stream (None), the others, most
+    work first, each on the least loaded of at most GPU_MAX_HW_QUEUES - 1 side
+    streams (_lib.side_streams).  Each side stream's classes run one after
+    another.  (A side stream on the caller's hardware queue, or two classes'
+    streams on one queue, measured up to 12% slower on the config-3 step.)"""
+    lanes: dict = {}
+    hw_queues = int(os.environ.get("GPU_MAX_HW_QUEUES", "4") or 4)
+    for dev in dict.fromkeys(c.device for c in calls):
+        keys = list(dict.fromkeys((c.device, c.group) for c in calls if c.device == dev))
+        keys.sort(key=lambda k: _class_flops(calls, k), reverse=True)
+        lanes[keys[0]] = None
+        rest = keys[1:]
+        if not rest:
+            continue
+        streams = _lib.side_streams(dev, max(1, min(len(rest), hw_queues - 1)))
+        load = [0.0] * len(streams)
+        for k in rest:
+            i = min(range(len(streams)), key=lambda j: load[j])
+            load[i] += _class_flops(calls, k)
+            lanes[k] = streams[i]
+    return lanes
+
+
 class _Call:
     """One batched ``mamw_muon_step`` launch group (matrices of one shape class)."""
 
@@ -318,7 +348,7 @@ class HipMuon:
         self._calls: list[_Call] = []
         self._ws: dict = {}  # device (in order) or (device, shape class) (concurrent) -> workspace
         self._concurrent = False
-        self._streams: dict = {}  # (device, shape class) -> side stream
+        self._lanes: dict = {}  # (device, shape class) -> side stream, or None: the caller's stream
 
     def _build_calls(self, active: list[nn.Parameter]) -> None:
         groups: dict[tuple, list[nn.Parameter]] = {}
@@ -374,6 +404,7 @@ class HipMuon:
             if ws is None or ws.numel() < nbytes:
                 self._ws[key] = None
                 self._ws[key] = torch.empty(nbytes, dtype=torch.uint8, device=key[0] if concurrent else key)
+        self._lanes = _lanes(calls) if concurrent else {}
         self._calls = calls
         self._concurrent = concurrent
 
@@ -440,25 +471,29 @@ class HipMuon:
                 ws.record_stream(cur)  # allocated under the stream current when the plan was built
                 launch(call, ws, cur.cuda_stream)
             return
-        # One side stream per shape class: each waits for the caller's current
-        # stream, runs its class's launches in order, and the current stream
-        # waits for all of them, so the step stays ordered with the caller's
-        # work on its stream.
-        forked = {}
+        # Concurrent shape classes (lanes from _lanes): the largest on the
+        # caller's current stream, the others on side streams.  Every side
+        # stream waits for the caller's stream before anything of this step is
+        # queued there, runs its classes' launches in order, and the caller's
+        # stream waits for all of them at the end, so the step stays ordered
+        # with the caller's work on its stream.
+        side = {}
         for call in self._calls:
-            key = (call.device, call.group)
-            s = self._streams.get(key)
-            if s is None:
-                s = self._streams[key] = torch.cuda.Stream(device=call.device)
-            if key not in forked:
+            s = self._lanes[(call.device, call.group)]
+            if s is not None and (call.device, id(s)) not in side:
+                side[(call.device, id(s))] = s
                 s.wait_stream(torch.cuda.current_stream(call.device))
-                self._ws[key].record_stream(s)
                 for t in amp_ptrs.get(call.device, ()):  # the scaler may drop its tensors after step()
                     if t is not None:
                         t.record_stream(s)
-                forked[key] = s
+        for call in self._calls:
+            key = (call.device, call.group)
+            s = self._lanes[key]
+            if s is None:
+                s = torch.cuda.current_stream(call.device)
+            self._ws[key].record_stream(s)
             launch(call, self._ws[key], s.cuda_stream)
-        for (dev, _), s in forked.items():
+        for (dev, _), s in side.items():
             torch.cuda.current_stream(dev).wait_stream(s)
 
     def zero_grad(self, set_to_none: bool = False):
