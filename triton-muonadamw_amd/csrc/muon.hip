@@ -259,8 +259,16 @@ __global__ __launch_bounds__(256) void muon_norm_kernel(const float* __restrict_
     __shared__ float red[4];
     const int tid = threadIdx.x, bat = blockIdx.x;
     const float* p = part + bat * P;
-    float s = 0.f;
-    for (int64_t i = tid; i < P; i += 256) s += p[i];
+    // Eight independent partial sums per thread (eight loads in flight, not
+    // one dependent chain), combined in a fixed order.
+    float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int64_t i = tid;
+    for (; i + 7 * 256 < P; i += 8 * 256) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a[u] += p[i + u * 256];
+    }
+    for (; i < P; i += 256) a[0] += p[i];
+    float s = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
     s = wave_sum(s);
     if ((tid & 63) == 0) red[tid >> 6] = s;
     __syncthreads();
