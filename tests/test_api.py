@@ -301,12 +301,11 @@ def test_launch_group_sizes_llama():
     assert group_sizes(0, 32, 4096, 4096, 256) == []
 
 
-@pytest.mark.parametrize("hw_queues,expect_streams", [("4", 3), ("2", 1), (None, 3)])
-def test_concurrent_class_lanes(monkeypatch, hw_queues, expect_streams):
+def test_concurrent_class_lanes(monkeypatch):
     """Concurrent shape classes: the class with the most Newton-Schulz work
-    runs on the caller's stream (lane None); the others, most work first, go to
-    the least loaded of at most GPU_MAX_HW_QUEUES - 1 side streams (4 queues
-    when unset); per device."""
+    runs on the caller's stream (lane None), every other class on one side
+    stream per device; the plan's launches are ordered by class work, most
+    first, each class's own launches in their original order."""
     from triton_muon_adamw import _lib
     from triton_muon_adamw.muon import hip_muon
     made = []
@@ -316,23 +315,12 @@ def test_concurrent_class_lanes(monkeypatch, hw_queues, expect_streams):
         return [f"{dev}/s{i}" for i in range(count)]
 
     monkeypatch.setattr(_lib, "side_streams", fake_side_streams)
-    if hw_queues is None:
-        monkeypatch.delenv("GPU_MAX_HW_QUEUES", raising=False)
-    else:
-        monkeypatch.setenv("GPU_MAX_HW_QUEUES", hw_queues)
     C = hip_muon._Call
     # (device, n matrices, m, n, class): work n * (3 m^2 n + m^3)
     calls = [C("d0", None, 1, 0, 768, 3072, 0), C("d0", None, 2, 0, 1024, 4096, 1), C("d0", None, 1, 0, 4096, 4096, 2),
              C("d0", None, 1, 0, 4096, 14336, 3), C("d0", None, 3, 0, 512, 512, 4), C("d1", None, 4, 0, 768, 768, 5),
-             C("d1", None, 1, 0, 768, 768, 6)]
+             C("d1", None, 1, 0, 768, 768, 6), C("d2", None, 1, 0, 256, 256, 7)]
     lanes = hip_muon._lanes(calls)
-    assert lanes[("d0", 3)] is None and lanes[("d1", 5)] is None
-    assert made == [("d0", min(4, expect_streams)), ("d1", 1)]
-    work = {k: hip_muon._class_flops(calls, k) for k in lanes}
-    d0 = sorted((k for k in lanes if k[0] == "d0" and lanes[k] is not None), key=lambda k: -work[k])
-    load = {f"d0/s{i}": 0.0 for i in range(expect_streams)}
-    for k in d0:  # longest first onto the least loaded stream (first of equals)
-        s = min(load, key=lambda name: (load[name], name))
-        assert lanes[k] == s, (k, lanes[k], s)
-        load[s] += work[k]
-    assert lanes[("d1", 6)] == "d1/s0"
+    assert lanes[("d0", 3)] is None and lanes[("d1", 5)] is None and lanes[("d2", 7)] is None
+    assert made == [("d0", 1), ("d1", 1)]
+    assert all(lanes[("d0", g)] == "d0/s0" for g in (0, 1, 2, 4)) and lanes[("d1", 6)] == "d1/s0"
