@@ -301,11 +301,19 @@ def test_launch_group_sizes_llama():
     assert group_sizes(0, 32, 4096, 4096, 256) == []
 
 
-def test_concurrent_class_lanes(monkeypatch):
-    """Concurrent shape classes: the class with the most Newton-Schulz work
-    runs on the caller's stream (lane None), every other class on one side
-    stream per device; the plan's launches are ordered by class work, most
-    first, each class's own launches in their original order."""
+@pytest.mark.parametrize("classes,n_side,caller,groups", [
+    # config 3: the 4096 x 14336 class on the caller's stream, the rest on one side stream
+    ([(1, 768, 3072), (2, 1024, 4096), (1, 4096, 4096), (1, 4096, 14336)], 1, 3, [[2, 1, 0]]),
+    # GPT-2: 24 x 768 x 3072 on the caller's stream
+    ([(12, 768, 2304), (12, 768, 768), (24, 768, 3072)], 1, 2, [[0, 1]]),
+    # the reference's hybrid MLP: batch-1 classes of small grids need a third lane
+    ([(1, 1024, 2048), (1, 2048, 4096), (1, 4096, 4096), (1, 1024, 4096)], 2, 2, [[1], [3, 0]]),
+])
+def test_concurrent_class_lanes(monkeypatch, classes, n_side, caller, groups):
+    """Concurrent shape classes: the class with the longest estimated time
+    (launch rounds, not flops) runs on the caller's stream (lane None); the
+    others, longest first, share the fewest side streams (up to 3) that all
+    finish within it.  ``groups`` lists each side stream's classes in order."""
     from triton_muon_adamw import _lib
     from triton_muon_adamw.muon import hip_muon
     made = []
@@ -315,12 +323,24 @@ def test_concurrent_class_lanes(monkeypatch):
         return [f"{dev}/s{i}" for i in range(count)]
 
     monkeypatch.setattr(_lib, "side_streams", fake_side_streams)
-    C = hip_muon._Call
-    # (device, n matrices, m, n, class): work n * (3 m^2 n + m^3)
-    calls = [C("d0", None, 1, 0, 768, 3072, 0), C("d0", None, 2, 0, 1024, 4096, 1), C("d0", None, 1, 0, 4096, 4096, 2),
-             C("d0", None, 1, 0, 4096, 14336, 3), C("d0", None, 3, 0, 512, 512, 4), C("d1", None, 4, 0, 768, 768, 5),
-             C("d1", None, 1, 0, 768, 768, 6), C("d2", None, 1, 0, 256, 256, 7)]
-    lanes = hip_muon._lanes(calls)
-    assert lanes[("d0", 3)] is None and lanes[("d1", 5)] is None and lanes[("d2", 7)] is None
-    assert made == [("d0", 1), ("d1", 1)]
-    assert all(lanes[("d0", g)] == "d0/s0" for g in (0, 1, 2, 4)) and lanes[("d1", 6)] == "d1/s0"
+    calls = [hip_muon._Call("d0", None, b, 0, m, n, g) for g, (b, m, n) in enumerate(classes)]
+    lanes, times = hip_muon._lanes(calls, 5, {"d0": 256})
+    assert lanes[("d0", caller)] is None
+    assert made == [("d0", n_side)]
+    by_stream = {}
+    for g in sorted(range(len(classes)), key=lambda g: -times[("d0", g)]):
+        if lanes[("d0", g)] is not None:
+            by_stream.setdefault(lanes[("d0", g)], []).append(g)
+    assert [by_stream[f"d0/s{i}"] for i in range(n_side)] == groups
+    side_time = [sum(times[("d0", g)] for g in grp) for grp in groups]
+    assert max(side_time) <= times[("d0", caller)]
+
+
+def test_concurrent_class_lanes_one_class_per_device(monkeypatch):
+    from triton_muon_adamw import _lib
+    from triton_muon_adamw.muon import hip_muon
+    monkeypatch.setattr(_lib, "side_streams", lambda dev, count: [f"{dev}/s{i}" for i in range(count)])
+    calls = [hip_muon._Call("d0", None, 2, 0, 512, 512, 0), hip_muon._Call("d1", None, 1, 0, 256, 256, 1),
+             hip_muon._Call("d1", None, 1, 0, 2048, 4096, 2)]
+    lanes, _ = hip_muon._lanes(calls, 5, {"d0": 256, "d1": 256})
+    assert lanes[("d0", 0)] is None and lanes[("d1", 2)] is None and lanes[("d1", 1)] == "d1/s0"

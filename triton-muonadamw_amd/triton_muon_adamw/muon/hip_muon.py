@@ -257,28 +257,69 @@ def group_sizes(count: int, cap: int, m: int, n: int, cus: int) -> list[int]:
     return sorted(best[count][2], reverse=True)
 
 
-def _class_flops(calls, key) -> float:
-    return sum(c.n * (3.0 * c.m * c.m * c.n_ + float(c.m) ** 3) for c in calls if (c.device, c.group) == key)
+def _launch_rounds(tiles: int, tile: int, k: int, cus: int) -> float:
+    """Time of one GEMM launch in k steps of a 256-wide tile: whole rounds of
+    the grid (two 128-wide workgroups per CU, a quarter of the work each)."""
+    slots = cus * (2 if tile == 128 else 1)
+    return math.ceil(tiles / slots) * (k / 64) * (1.0 if tile == 256 else 0.5)
 
 
-def _lanes(calls) -> dict:
-    """Streams of concurrent shape classes, per device: the class with the
-    most Newton-Schulz work on the caller's stream (None), every other class
-    on one side stream of the library's own (_lib.side_streams), where they
-    run one after another, most work first (the caller sorts its launches so).
-    Measured on the config-3 and GPT-2 steps: 4.91 and 1.80 ms against 5.01
-    and 1.81 ms with one side stream per class (up to three), 5.62 and 1.89 ms
-    with only the second largest class beside the largest."""
+def _class_time(calls, key, steps: int, cus: int) -> float:
+    """Estimated Newton-Schulz time of one shape class (its launch groups one
+    after another): a launch whose grid fills a fraction of the GPU still
+    takes a round, which is what makes a class of small grids slow for its
+    flops."""
+    t = 0.0
+    for c in calls:
+        if (c.device, c.group) != key:
+            continue
+        tile = gemm_tile(c.m, c.n_, c.n)
+        mp, np_ = -(-c.m // tile) * tile, -(-c.n_ // tile) * tile
+        tm = mp // tile
+        sym = c.n * tm * (tm + 1) // 2  # Gram and polynomial tiles (lower triangle)
+        utile = 256 if (tile == 128 and c.m >= 1024 and mp % 256 == 0 and np_ % 256 == 0) else tile
+        upd = c.n * (mp // utile) * (np_ // utile)
+        t += steps * (_launch_rounds(sym, tile, np_, cus) + _launch_rounds(sym, tile, mp, cus)
+                      + _launch_rounds(upd, utile, mp, cus))
+    return t
+
+
+def _lanes(calls, steps: int, cus: dict) -> tuple[dict, dict]:
+    """Streams of concurrent shape classes, per device, and each class's
+    estimated time (_class_time).  The longest class runs on the caller's
+    stream (None); the others, longest first, each on the least loaded of
+    L - 1 side streams of the library's own (_lib.side_streams), where a side
+    stream's classes run one after another.  L is the fewest lanes (2 to 4)
+    whose side streams all finish within the caller's class; more concurrent
+    streams than that only contend.  Measured: config 3 (the 4096 x 14336
+    class against four smaller ones) 4.91 ms with two lanes against 5.01 with
+    one side stream per class; GPT-2 1.80 against 1.81; the reference's hybrid
+    MLP (four batch-1 classes whose grids mostly underfill the GPU) needs
+    three."""
     lanes: dict = {}
+    times: dict = {}
     for dev in dict.fromkeys(c.device for c in calls):
         keys = list(dict.fromkeys((c.device, c.group) for c in calls if c.device == dev))
-        keys.sort(key=lambda k: _class_flops(calls, k), reverse=True)
+        for k in keys:
+            times[k] = _class_time(calls, k, steps, cus[dev])
+        keys.sort(key=lambda k: times[k], reverse=True)
         lanes[keys[0]] = None
-        if len(keys) > 1:
-            side = _lib.side_streams(dev, 1)[0]
-            for k in keys[1:]:
-                lanes[k] = side
-    return lanes
+        rest = keys[1:]
+        if not rest:
+            continue
+        for n_side in range(1, min(3, len(rest)) + 1):
+            load = [0.0] * n_side
+            pick = []
+            for k in rest:
+                i = min(range(n_side), key=lambda j: load[j])
+                load[i] += times[k]
+                pick.append(i)
+            if max(load) <= times[keys[0]]:
+                break
+        streams = _lib.side_streams(dev, n_side)
+        for k, i in zip(rest, pick):
+            lanes[k] = streams[i]
+    return lanes, times
 
 
 class _Call:
@@ -399,10 +440,11 @@ class HipMuon:
             if ws is None or ws.numel() < nbytes:
                 self._ws[key] = None
                 self._ws[key] = torch.empty(nbytes, dtype=torch.uint8, device=key[0] if concurrent else key)
-        self._lanes = _lanes(calls) if concurrent else {}
-        if concurrent:  # most work first; a class's own launches keep their order (stable sort)
-            work = {k: _class_flops(calls, k) for k in self._lanes}
-            calls.sort(key=lambda c: -work[(c.device, c.group)])
+        self._lanes = {}
+        if concurrent:  # longest class first; a class's own launches keep their order (stable sort)
+            cus = {d: torch.cuda.get_device_properties(d).multi_processor_count for d in dict.fromkeys(c.device for c in calls)}
+            self._lanes, times = _lanes(calls, self.steps, cus)
+            calls.sort(key=lambda c: -times[(c.device, c.group)])
         self._calls = calls
         self._concurrent = concurrent
 
