@@ -342,13 +342,15 @@ class HipMuon:
     # than groups of 20).  Within the cap, group_sizes() picks the split.
     workspace_limit_bytes: int | None = None
     # A step whose Newton-Schulz work (sum of ns_steps*(3 m^2 n + m^3)) is at
-    # most this many flops runs its shape classes concurrently, one side
-    # stream and one workspace each: their launches are too small to fill the
-    # GPU one after another (measured: GPT-2 Muon step -10%, config-3 -17%).
-    # Larger steps run the classes in order, which keeps each class's
-    # operands in the L2 and memory-side cache (concurrent classes measured
-    # slower on the Llama-8B step).
-    concurrent_flops_limit = 2e13
+    # most this many flops runs its shape classes concurrently (lanes from
+    # _lanes, one workspace per class): their launches are too small to fill
+    # the GPU one after another (measured: GPT-2 Muon step -10%, config-3
+    # -17%).  Larger steps run the classes in order, which keeps each class's
+    # operands in the L2 and memory-side cache.  Measured on the first L
+    # layers of the Llama-8B set, concurrent against in order: L = 1 (1.4e13)
+    # 13.19 vs 14.10 ms, L = 2 (3.0e13) 26.46 vs 26.73, L = 4 (5.9e13) 52.72 vs
+    # 52.10, L = 8 (1.2e14) 105.9 vs 102.9, all 32 layers 405 vs 391.
+    concurrent_flops_limit = 4e13
 
     def __init__(
         self,
