@@ -210,11 +210,22 @@ def test_tile_edge_does_not_change_the_bits(gpu):
         assert torch.equal(opt.momentum[a], o.momentum[b])
 
 
+# Shape classes of a small step: three (two side streams beside the caller's),
+# and five whose estimated times make _lanes use three side streams
+# (tests/test_api.py checks that split on the CPU).
+CONCURRENT_SETS = {
+    "three_classes": [(256, 512)] * 3 + [(512, 256)] * 2 + [(384, 384)] * 2 + [(128, 640)],
+    "five_classes": [(256, 512), (512, 256), (384, 384)] * 1 + [(384, 384), (128, 640), (640, 128), (320, 448),
+                                                                (448, 320), (192, 576), (576, 192)],
+}
+
+
+@pytest.mark.parametrize("classes", sorted(CONCURRENT_SETS))
 @pytest.mark.parametrize("on_side_stream", [False, True])
-def test_concurrent_classes_equal_in_order(gpu, on_side_stream):
+def test_concurrent_classes_equal_in_order(gpu, on_side_stream, classes):
     """Shape classes on their own streams (small steps) give the same bits as one after another,
     also when the caller steps on a non-default stream and reads the result there."""
-    shapes = [(256, 512)] * 3 + [(512, 256)] * 2 + [(384, 384)] * 2 + [(128, 640)]
+    shapes = CONCURRENT_SETS[classes]
     ps, gs, ms = muon_inputs(shapes, seed=7)
     runs = []
     for limit in (0.0, HipMuon.concurrent_flops_limit):
@@ -233,6 +244,9 @@ def test_concurrent_classes_equal_in_order(gpu, on_side_stream):
             for _ in range(3):
                 opt.step()
             assert opt._concurrent == (limit > 0)
+            if limit > 0:
+                side = {id(st) for st in opt._lanes.values() if st is not None}
+                assert len(side) == (3 if classes == "five_classes" else 2)
             out = [q.detach().clone() for q in params] + [opt.momentum[q].clone() for q in params]
         torch.cuda.current_stream(gpu).wait_stream(stream)
         runs.append(out)
@@ -298,6 +312,43 @@ def test_config3_ns_vs_torch(gpu, shape):
     err = (out - ref).norm().item() / ref.norm().item()
     assert err <= 1e-2, f"{shape}: NS rel err vs torch {err}"
 
+
+
+def test_config3_concurrent_step_vs_torch(gpu):
+    """Config 3 as bench.py times it: the five matrices in one HipMuon.step(),
+    whose four shape classes run concurrently (the longest on the caller's
+    stream, the others on side streams), with the seeded values of
+    bench_ns_c3 (params N(0, 0.02), gradients N(0, 1), momentum N(0, 1e-3)).
+    Every matrix: momentum within 2 ulp of torch's lerp_, and the update
+    against torch's Newton-Schulz of the same Nesterov blend, relative
+    Frobenius error <= 1e-2 (muon_benchmark.py:105)."""
+    from helpers import C3_SHAPES
+    from torch.optim._muon import _zeropower_via_newtonschulz
+
+    gen = torch.Generator(device=gpu).manual_seed(1)
+    params = []
+    for s in C3_SHAPES:
+        p = torch.nn.Parameter(torch.empty(s, device=gpu).normal_(0.0, 0.02, generator=gen))
+        p.grad = torch.empty(s, device=gpu).normal_(0.0, 1.0, generator=gen)
+        params.append(p)
+    opt = HipMuon(params, lr=1e-3, weight_decay=0.1, coeffs=COEFFS, nesterov=True, beta=0.95, ns_steps=5, eps=1e-7)
+    for p in params:
+        opt.momentum[p].normal_(0.0, 1e-3, generator=gen)
+    p0 = [p.detach().clone() for p in params]
+    m0 = [opt.momentum[p].clone() for p in params]
+    opt.step()
+    torch.cuda.synchronize()
+    assert opt._concurrent and len({c.group for c in opt._calls}) == 4
+    assert any(st is not None for st in opt._lanes.values())
+    keep = 1 - 1e-3 * 0.1
+    for q0, p, mom0 in zip(p0, params, m0):
+        g = p.grad
+        mom = mom0.lerp(g, 1 - 0.95)
+        torch.testing.assert_close(opt.momentum[p], mom, atol=0, rtol=2.4e-7)
+        ref = _zeropower_via_newtonschulz(g.lerp(mom, 0.95), COEFFS, 5, 1e-7).double()
+        u = (q0.double() * keep - p.detach().double()) / scaled_lr(1e-3, "original", *p.shape)
+        err = ((u - ref).norm() / ref.norm()).item()
+        assert err <= 1e-2, f"{tuple(p.shape)}: update rel err {err} against torch's Newton-Schulz"
 
 
 def _orthogonal_signs(rows, cols, rng):

@@ -437,13 +437,15 @@ struct GemmArgs {
 // neighbouring patches, so the round's operands are one matrix's worth and stay
 // in the memory-side cache.  An incomplete last round (all of a grid smaller
 // than 8 x 32) is cut into 8 contiguous ranges, one per XCD.  Logical order
-// within a matrix: groups of kGroupM tile rows, column by column (symmetric
-// products: only the tiles with ti <= tj).
+// within a matrix: groups of GM tile rows, column by column (symmetric
+// products: only the tiles with ti <= tj).  GM = 4 for 256-wide tiles; 8 for
+// 128-wide tiles, whose rounds hold twice the blocks (two per CU), so that an
+// XCD's share of a small matrix (m = 768: all six tile rows) reads each X^T
+// panel once (GPT-2's updates 4% faster than with groups of 4, Grams 1%).
 constexpr int kXcds = 8;
 constexpr int kXcdSlots = 32;
-constexpr int kGroupM = 4;
 
-template <bool SYM>
+template <bool SYM, int kGroupM>
 __device__ __forceinline__ void decode_tile(const GemmArgs& g, int& bat, int& ti, int& tj) {
     const int L = blockIdx.x, total = gridDim.x;
     const int full = (total / (kXcds * kXcdSlots)) * (kXcds * kXcdSlots);
@@ -632,7 +634,7 @@ __global__ __launch_bounds__(kGemmThreads, BM == 128 ? 2 : 1) void ns_gemm_kerne
         if (g.found_inf && *g.found_inf != 0.0f) return;  // uniform per launch: the whole block leaves
     }
     int bat, ti, tj;
-    decode_tile<SYM>(g, bat, ti, tj);
+    decode_tile<SYM, BM == 128 ? 8 : 4>(g, bat, ti, tj);
     // Uniform by construction; pinned to scalar registers so that every
     // buffer resource derived from them is one (a resource the compiler
     // cannot prove uniform turns each load into a loop over the lanes).

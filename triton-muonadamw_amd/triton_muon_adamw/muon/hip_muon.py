@@ -307,19 +307,30 @@ def _lanes(calls, steps: int, cus: dict) -> tuple[dict, dict]:
         rest = keys[1:]
         if not rest:
             continue
-        for n_side in range(1, min(3, len(rest)) + 1):
-            load = [0.0] * n_side
-            pick = []
-            for k in rest:
-                i = min(range(n_side), key=lambda j: load[j])
-                load[i] += times[k]
-                pick.append(i)
-            if max(load) <= times[keys[0]]:
-                break
+        n_side, pick = _lane_split([times[k] for k in keys])
         streams = _lib.side_streams(dev, n_side)
         for k, i in zip(rest, pick):
             lanes[k] = streams[i]
     return lanes, times
+
+
+def _lane_split(times: list[float]) -> tuple[int, list[int]]:
+    """The side-stream split of _lanes for class times sorted longest first:
+    the first class stays on the caller's stream; returns the number of side
+    streams (1 to 3) and, for each later class, the side stream it joins (the
+    least loaded so far).  The fewest side streams whose loads all fit within
+    the first class's time; three when none does."""
+    rest = times[1:]
+    for n_side in range(1, min(3, len(rest)) + 1):
+        load = [0.0] * n_side
+        pick = []
+        for t in rest:
+            i = min(range(n_side), key=lambda j: load[j])
+            load[i] += t
+            pick.append(i)
+        if max(load) <= times[0]:
+            break
+    return n_side, pick
 
 
 class _Call:

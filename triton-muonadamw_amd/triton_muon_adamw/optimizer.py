@@ -117,9 +117,10 @@ def split_parameters(
 class MuonAdamW(HipMuon, HipAdamW, torch.optim.Optimizer):
     """Hybrid optimizer: Muon for 2-D weight matrices, AdamW for the rest.
 
-    Two-dimensional parameters are updated with Muon, except the input
-    embedding and the output head; all other trainable parameters (biases,
-    normalisation weights, embeddings) use the AdamW branch.
+    The Muon branch takes the weight matrices (every 2-D parameter other
+    than the token embedding and the LM head); the AdamW branch takes what is
+    left: vectors such as biases and norm gains, and the embedding and head
+    matrices themselves.
 
     Parameters
     ----------
