@@ -16,7 +16,13 @@ same JSON line:
 * ns     : Muon-only step on the config 3 matrices, NS TFLOP/s and % of peak over the step's device time
 * vs_torch_gpu : the reference's own comparison on this GPU (event-timed step
            loops as in its benchmark scripts): this build against
-           PyTorchMuonAdamW / fused torch AdamW on the same parameters
+           PyTorchMuonAdamW (eager and torch.compile'd) / fused torch AdamW on
+           the same parameters
+* peak_mem : device memory each optimizer (this build, PyTorchMuonAdamW) adds
+           to the resident GPT-2 and Llama-8B parameter sets
+* c1_step_ms : config 1 (toy MLP) step on the GPU
+
+`cpu_baseline.configs` times configs 1-4 in full on the same host cores.
 
 `roofline` describes the dominant kernel of the headline step (the one with
 the largest total device time).  `cpu_baseline` times this build's
@@ -181,17 +187,51 @@ def log_kernels(label, agg, steps):
         log(f"    {k:42s} {a['launches']:4d} launches {a['ms'] / steps:9.3f} ms/step  {tf:8.1f} TFLOP/s")
 
 
-def bench_full_step(layout, dev, steps, warmup, seed, label, keep_host=None, profile_in_order=False):
+def optimizer_memory(make_opt, dev, label):
+    """Device memory an optimizer adds to a resident parameter set (the
+    reference benchmarks print torch.cuda.max_memory_allocated,
+    muon_adamw_benchmark.py:149-151): `held_gb`, what it keeps between steps
+    (state, workspace), measured after its first step; `peak_gb`, the most
+    allocated at once during a later step, both above the parameters and
+    gradients."""
+    import torch
+
+    torch.cuda.synchronize(dev)
+    torch.cuda.empty_cache()
+    base = torch.cuda.memory_allocated(dev)
+    opt = make_opt()
+    opt.step()  # the first step allocates lazily created state and workspace
+    torch.cuda.synchronize(dev)
+    held = torch.cuda.memory_allocated(dev) - base
+    torch.cuda.reset_peak_memory_stats(dev)
+    opt.step()
+    torch.cuda.synchronize(dev)
+    peak = torch.cuda.max_memory_allocated(dev) - base
+    out = {"held_gb": round(held / 1e9, 3), "peak_gb": round(peak / 1e9, 3)}
+    ws = getattr(getattr(opt, "muon", None), "_ws", None)
+    if isinstance(ws, dict):
+        out["muon_workspace_gb"] = round(sum(w.numel() for w in ws.values()) / 1e9, 3)
+    log(f"[{label}] memory: {out}")
+    del opt
+    torch.cuda.synchronize(dev)
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_full_step(layout, dev, steps, warmup, seed, label, keep_host=None, profile_in_order=False,
+                    memory=False):
     """Clean timed pass (`value`), then a profiled pass of the same length.
 
     `keep_host(named)` (optional) copies what the CPU baseline needs to host
     memory before the first step.  `profile_in_order`: the profiled pass runs
     the Muon shape classes in order (the clean pass keeps the library's
-    choice), so that per-kernel durations do not overlap.
+    choice), so that per-kernel durations do not overlap.  `memory`: after
+    the passes, the device memory this build's optimizer and PyTorchMuonAdamW
+    each add to the same resident parameters (optimizer_memory).
     """
     import torch
 
-    from triton_muon_adamw import MuonAdamW
+    from triton_muon_adamw import MuonAdamW, PyTorchMuonAdamW
 
     mc, ac = configs()
     named = make_params(layout, dev, seed)
@@ -210,9 +250,43 @@ def bench_full_step(layout, dev, steps, warmup, seed, label, keep_host=None, pro
     log(f"[{label}] profiled pass: {pms:.3f} ms/step with an event pair per dispatch"
         f"{' (shape classes in order)' if profile_in_order and conc else ''}")
     log_kernels(label, agg, steps)
+    del opt
+    mem = None
+    if memory:
+        mem = {"this_build": optimizer_memory(lambda: MuonAdamW(split(named), muon_config=mc, adam_config=ac,
+                                                                 parameter_split="explicit"), dev, label),
+               "torch_wrapper": optimizer_memory(lambda: PyTorchMuonAdamW(split(named), muon_config=mc,
+                                                                          adam_config=ac,
+                                                                          parameter_split="explicit"),
+                                                 dev, label + " PyTorchMuonAdamW"),
+               "params_and_grads_gb": round(sum(2 * p.numel() * p.element_size() for _, p, _ in named) / 1e9, 3)}
+    del named
+    torch.cuda.empty_cache()
+    return ms, pms, agg, host, mem
+
+
+def c1_layout():
+    """Config 1: Linear(512, 2048) -> LayerNorm(2048) -> Linear(2048, 512), torch Linear layout."""
+    return [("fc1.w", (2048, 512), "muon"), ("fc1.b", (2048,), "adam"), ("ln.w", (2048,), "adam"),
+            ("ln.b", (2048,), "adam"), ("fc2.w", (512, 2048), "muon"), ("fc2.b", (512,), "adam")]
+
+
+def bench_c1(dev, seed: int):
+    """Config 1 (the toy MLP of BASELINE config 1) on the GPU: one MuonAdamW step, ms (event loop of
+    20 steps after 5 warm-up)."""
+    import torch
+
+    from triton_muon_adamw import MuonAdamW
+
+    mc, _ = configs()
+    _, ac = configs()
+    named = make_params(c1_layout(), dev, seed)
+    opt = MuonAdamW(split(named), muon_config=mc, adam_config=ac, parameter_split="explicit")
+    ms = event_loop_ms(opt.step, 5, 20)
+    log(f"[c1] toy MLP step {ms:.4f} ms")
     del opt, named
     torch.cuda.empty_cache()
-    return ms, pms, agg, host
+    return round(ms, 4)
 
 
 def bench_adamw_c2(dev, steps, warmup):
@@ -414,6 +488,59 @@ def cpu_baseline(sample, budget_s: float = 30.0):
     }
 
 
+def cpu_baseline_configs(threads: int):
+    """Configs 1-4 on the host CPU with the reference's torch.optim path, median of 3 timed steps after
+    one warm-up step (config 3: of 2): config 1 (toy MLP) and config 4 (GPT-2 set) through
+    PyTorchMuonAdamW, config 2 through fused torch.optim.AdamW (the reference's AdamW comparison,
+    adam_benchmark.py:35-42), config 3 through torch.optim.Muon (muon_benchmark.py:33-34).  Values:
+    seeded N(0, 0.02) parameters and N(0, 1e-3) gradients (config 3: N(0, 1)), drawn on the CPU."""
+    import torch
+
+    from helpers import C3_SHAPES, c2_sizes, gpt2_layout
+    from triton_muon_adamw import PyTorchMuonAdamW
+
+    torch.set_num_threads(max(1, threads))
+    mc, ac = configs()
+    gen = torch.Generator().manual_seed(0)
+
+    def params(shapes, gstd=1e-3):
+        out = []
+        for s in shapes:
+            p = torch.nn.Parameter(torch.randn(s, generator=gen) * 0.02)
+            p.grad = torch.randn(s, generator=gen) * gstd
+            out.append(p)
+        return out
+
+    def wrapper(layout):
+        ps = params([s for _, s, _ in layout])
+        d = {"adam": [p for p, (_, _, b) in zip(ps, layout) if b == "adam"],
+             "muon": [p for p, (_, _, b) in zip(ps, layout) if b == "muon"]}
+        return PyTorchMuonAdamW(d, muon_config=mc, adam_config=ac, parameter_split="explicit")
+
+    cases = {
+        "c1_toy_mlp": (lambda: wrapper(c1_layout()), 3),
+        "c2_adamw": (lambda: torch.optim.AdamW(params([(n,) for n in c2_sizes()]), lr=ac.lr, betas=ac.betas,
+                                               eps=ac.eps, weight_decay=ac.weight_decay, fused=True), 3),
+        "c3_ns": (lambda: torch.optim.Muon(params(C3_SHAPES, gstd=1.0), lr=mc.lr, momentum=mc.beta,
+                                           weight_decay=mc.weight_decay, nesterov=mc.nesterov,
+                                           ns_coefficients=tuple(mc.coeffs), eps=mc.eps, ns_steps=mc.ns_steps), 2),
+        "c4_gpt2": (lambda: wrapper(gpt2_layout()), 3),
+    }
+    out = {}
+    for name, (make, n) in cases.items():
+        opt = make()
+        opt.step()  # warm-up (allocates the state)
+        times = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            opt.step()
+            times.append(time.perf_counter() - t0)
+        out[name] = {"ms": round(statistics.median(times) * 1e3, 2), "timed_steps": n}
+        log(f"[cpu baseline] {name}: median {out[name]['ms']} ms of {n} steps")
+        del opt
+    return out
+
+
 def bench_vs_torch_gpu(dev, seed: int = 0):
     """The reference's own comparison, on this GPU, with its event-timed loop.
 
@@ -423,10 +550,10 @@ def bench_vs_torch_gpu(dev, seed: int = 0):
 
     * ref_hybrid_mlp: the reference's hybrid benchmark model
       (muon_adamw_benchmark.py:9-20,28-39,41-52; 2-D weights to Muon), this
-      build's MuonAdamW against PyTorchMuonAdamW (eager: the reference also
-      times a torch.compile'd wrapper step, which is not rebuilt here);
-      warm-up 50, 100 timed steps, mean of 5 loops (:99-126).  Published:
-      1.24-1.26x (README.md:48).
+      build's MuonAdamW against PyTorchMuonAdamW, eager and, as the reference
+      times it, compiled by torch.compile (inductor); warm-up 50, 100 timed
+      steps, mean of 5 loops (:99-126).  Published: 1.24-1.26x against the
+      compiled step (README.md:48).
     * ref_adamw_mlp: the reference's AdamW benchmark model
       (adam_benchmark.py:14-25,33-42), HipAdamW against fused torch AdamW;
       warm-up 100, 500 timed steps, mean of 10 loops (:75-108).  Published:
@@ -478,8 +605,22 @@ def bench_vs_torch_gpu(dev, seed: int = 0):
     a, b = twin(mlp_shapes([1024, 2048, 4096, 4096, 1024]))
     mine = MuonAdamW(a, muon_config=mc_ref, adam_config=ac_ref, parameter_split="explicit")
     ref = PyTorchMuonAdamW(b, muon_config=mc_ref, adam_config=ac_ref, parameter_split="explicit")
-    r = ratio(event_loop_ms(mine.step, 50, 100, 5), event_loop_ms(ref.step, 50, 100, 5))
+    mine_ms = event_loop_ms(mine.step, 50, 100, 5)
+    r = ratio(mine_ms, event_loop_ms(ref.step, 50, 100, 5))
     r["published_speedup"] = "1.24-1.26 (vs the torch.compile'd wrapper step)"
+    # The reference's own comparison point: torch.compile(pytorch_optimizer.step)
+    # (muon_adamw_benchmark.py:66,123), compiled here by inductor for this GPU.
+    try:
+        t0 = time.perf_counter()
+        compiled = torch.compile(ref.step)
+        compiled()
+        torch.cuda.synchronize(dev)
+        r["compile_s"] = round(time.perf_counter() - t0, 1)
+        c_ms = event_loop_ms(compiled, 50, 100, 5)
+        r["compiled_torch_ms"] = round(c_ms, 4)
+        r["speedup_vs_compiled"] = round(c_ms / mine_ms, 3)
+    except Exception as e:  # inductor is optional: record why the compiled point is missing
+        r["compiled_torch_error"] = f"{type(e).__name__}: {str(e)[:200]}"
     out["ref_hybrid_mlp"] = r
     log(f"[vs torch gpu] reference hybrid MLP: {r}")
     # reference AdamW benchmark (adam_benchmark.py:33-42)
@@ -567,8 +708,8 @@ def main():
         return
     layout = llama8b_layout()
     keep = None if args.no_cpu else llama_cpu_sample
-    ms, pms, agg, sample = bench_full_step(layout, dev, args.steps, args.warmup, args.seed, "llama8b",
-                                           keep_host=keep)
+    ms, pms, agg, sample, l_mem = bench_full_step(layout, dev, args.steps, args.warmup, args.seed, "llama8b",
+                                                  keep_host=keep, memory=not args.no_extras)
     dom_name, dom = max(agg.items(), key=lambda kv: kv[1]["ms"])
     achieved = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
     roofline = {
@@ -599,8 +740,8 @@ def main():
                           "kernels": per_kernel}}
     if not args.no_extras:
         g_steps, g_warm = max(args.steps, 20), max(args.warmup, 5)
-        g_ms, g_pms, g_agg, _ = bench_full_step(gpt2_layout(), dev, g_steps, g_warm, args.seed, "gpt2",
-                                                profile_in_order=True)
+        g_ms, g_pms, g_agg, _, g_mem = bench_full_step(gpt2_layout(), dev, g_steps, g_warm, args.seed, "gpt2",
+                                                       profile_in_order=True, memory=True)
         g_ns = [a for k, a in g_agg.items() if k.startswith("ns_gemm_kernel")]
         g_ns_ms = sum(a["ms"] for a in g_ns) / g_steps
         g_ns_fl = sum(a["flops"] for a in g_ns) / g_steps
@@ -614,6 +755,12 @@ def main():
                                                    **({"TFLOP/s": round(a["flops"] / (a["ms"] * 1e-3) / 1e12, 1)}
                                                       if a["flops"] else {})}
                                                for k, a in sorted(g_agg.items(), key=lambda kv: -kv[1]["ms"])}}
+        extras["peak_mem"] = {
+            "note": "device memory each optimizer adds to the resident fp32 parameters and gradients: held_gb "
+                    "between steps (state, workspace), peak_gb at most during a step, both above the "
+                    "parameters and gradients",
+            "llama8b": l_mem, "gpt2": g_mem}
+        extras["c1_step_ms"] = bench_c1(dev, args.seed)
         extras["adamw_c2"] = bench_adamw_c2(dev, max(args.steps, 20), max(args.warmup, 3))
         extras["ns_c3"] = bench_ns_c3(dev, args.steps, args.warmup)
         extras["llama_kv_class"] = bench_kv_class(dev, args.steps, args.warmup)
@@ -623,6 +770,9 @@ def main():
         log("[cpu baseline] PyTorchMuonAdamW on host CPU (bounded sample) ...")
         cpu = cpu_baseline(sample)
         log(f"[cpu baseline] {cpu['value']} ms extrapolated; {cpu['sample']}")
+        cpu["configs"] = cpu_baseline_configs(cpu["cores"])
+        cpu["configs_note"] = ("configs 1-4 in full on the same host cores: median ms per step (the reference's "
+                               "torch.optim path; config 2 fused AdamW, config 3 torch Muon)")
     line = {
         "metric": METRIC,
         "value": round(ms, 3),
