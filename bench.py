@@ -63,7 +63,9 @@ def kernel_label(name: str, variant: int) -> str:
     if name.startswith("ns_gemm_kernel:"):
         mode = name.split(":")[1]
         flags = ["true" if (variant >> b) & 1 else "false" for b in range(3)]  # k-blocked, k-major, lower A
-        return f"ns_gemm_kernel<{variant // 8}, {MODE_NUM[mode]}, {', '.join(flags)}>"
+        tile = variant // 8  # 128, 256, or 192 for the 128 x 192 update tile
+        bm, bn = (128, 192) if tile == 192 else (tile, tile)
+        return f"ns_gemm_kernel<{bm}, {MODE_NUM[mode]}, {', '.join(flags)}, {bn}>"
     return name
 
 

@@ -171,6 +171,42 @@ def test_batched_equals_single(gpu):
         assert torch.equal(a.detach(), b.detach())
 
 
+def test_rect_tile_does_not_change_the_bits(gpu):
+    """Twelve 768 x 3072 matrices (the tall and the wide orientation) in one
+    launch group run their updates on 128 x 192 tiles (1152 tiles, at least
+    two rounds); each alone runs them on 128 x 128 tiles.  Every output
+    element sums the same products in the same order under either tile, so
+    parameters and momenta agree bit for bit (two steps)."""
+    from triton_muon_adamw import _lib
+    shapes = [(768, 3072)] * 6 + [(3072, 768)] * 6
+    ps, gs, ms, params, opt = _run_muon(shapes, gpu, seed=12)
+    singles = []
+    for p, g, m in zip(ps, gs, ms):
+        q = torch.nn.Parameter(p.to(gpu))
+        q.grad = g.to(gpu)
+        o = HipMuon([q], lr=opt.lr, coeffs=COEFFS)
+        o.momentum[q].copy_(m)
+        singles.append((q, o))
+
+    def tiles_of(step_fn):
+        _lib.prof_start()
+        step_fn()
+        _lib.prof_stop()
+        return {(r["kernel"].split(":")[1], r["variant"] // 8) for r in _lib.prof_collect()
+                if r["kernel"].startswith("ns_gemm")}
+
+    assert tiles_of(opt.step) == {("gram", 128), ("poly", 128), ("update", 192), ("apply", 192)}
+    assert tiles_of(lambda: [o.step() for _, o in singles]) == {("gram", 128), ("poly", 128), ("update", 128),
+                                                                ("apply", 128)}
+    opt.step()
+    for q, o in singles:
+        o.step()
+    torch.cuda.synchronize()
+    for a, (b, o) in zip(params, singles):
+        assert torch.equal(a.detach(), b.detach())
+        assert torch.equal(opt.momentum[a], o.momentum[b])
+
+
 def test_tile_edge_does_not_change_the_bits(gpu):
     """Eight 1024 x 2048 matrices in one launch group run on 256-wide tiles
     (m >= 1024 and 8 matrices) with lower-triangle A and B; each alone runs
