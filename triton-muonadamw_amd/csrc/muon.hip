@@ -552,6 +552,34 @@ __device__ __forceinline__ void apply_begin(const MuonMatDesc& d, ApplyPiece& a,
     }
 }
 
+// apply_begin through a buffer resource `rp` over the parameter elements from
+// element `base` on: every piece issues exactly its loads (two 16-byte loads
+// for an fp32 parameter, one for bf16), those of a piece that apply_end will
+// not read whole (ragged or unaligned, or outside the matrix) at an offset past
+// the resource's end, which reads zeros without touching memory.  A caller can
+// then wait for older loads with a fixed vmcnt while these stay in flight.
+template <bool NT = false>
+__device__ __forceinline__ void apply_begin_buf(const MuonMatDesc& d, ApplyPiece& a, int64_t prow, int64_t pcol,
+                                                int64_t cap, int64_t left, __amdgpu_buffer_rsrc_t rp,
+                                                int64_t base) {
+    const int64_t nv = cap < left ? cap : left;
+    a.nv = nv > 0 ? int(nv) : 0;
+    a.idx = prow * d.cols + pcol;
+    const bool bf = (d.flags & MAMW_BF16_PARAM) != 0;
+    const uintptr_t pa = bf ? reinterpret_cast<uintptr_t>(reinterpret_cast<uint16_t*>(d.param) + a.idx)
+                            : reinterpret_cast<uintptr_t>(d.param + a.idx);
+    const uintptr_t ua = d.upd ? reinterpret_cast<uintptr_t>(d.upd + a.idx) : 0;
+    a.fast = a.nv == 8 && ((pa | ua) & 15) == 0;
+    const int off = a.fast ? int((a.idx - base) * (bf ? 2 : 4)) : 0x7FFFFF00;
+    typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+    const u32x4_t v0 = __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, NT ? 2 : 0);
+    a.p0 = make_uint4(v0.x, v0.y, v0.z, v0.w);
+    if (!bf) {
+        const u32x4_t v1 = __builtin_amdgcn_raw_buffer_load_b128(rp, off + 16, 0, NT ? 2 : 0);
+        a.p1 = make_uint4(v1.x, v1.y, v1.z, v1.w);
+    }
+}
+
 template <bool NT = false>
 __device__ __forceinline__ void apply_end(const MuonMatDesc& d, const ApplyPiece& a, float keep) {
     if (a.nv == 0) return;
@@ -1038,7 +1066,7 @@ __global__ __launch_bounds__(kGemmThreads, BM == 128 ? 2 : 1) void ns_gemm_kerne
     const bool diag = SYM && ti == tj;
     __syncthreads();  // every wave is done with the stage buffers
 
-    if constexpr (MODE != MODE_GRAM) {
+    if constexpr (MODE != MODE_GRAM && MODE != MODE_APPLY) {
         // The rest of the coefficient tile (the blocks in stage buffer 1).
         constexpr int NREST = (NSB - NPRE) / 4;  // per wave
 #pragma unroll
@@ -1244,6 +1272,99 @@ __global__ __launch_bounds__(kGemmThreads, BM == 128 ? 2 : 1) void ns_gemm_kerne
         return;
     }
 
+    if constexpr (MODE == MODE_APPLY) {
+        // APPLY: the parameter's own orientation, from TT rows (a tall
+        // matrix: parameter row tj*BN + x holds TT row x) or gathered from TT
+        // columns (a wide one), U pieces of 8 elements per thread at a time.
+        // The first batch's parameter loads go out before the coefficient
+        // wait and the combine, so their HBM latency passes under them: the
+        // rest of the coefficient tile is issued first, and the wait lets
+        // exactly those parameter loads stay in flight (apply_begin_buf
+        // issues a fixed number per piece).  No fence from here on: the
+        // barriers wait for LDS only (lgkmcnt), so the loads stay in flight.
+        constexpr int U = NT % 8 == 0 ? 8 : 6;  // pieces per batch (NT == NIT pieces per thread)
+        static_assert(NT == NIT && NT % U == 0, "whole batches");
+        constexpr int NREST = (NSB - NPRE) / 4;  // per wave
+        const bool bf = (d.flags & MAMW_BF16_PARAM) != 0;
+        // Parameter elements the tile covers, from `base` on (rows tj*BN.. of
+        // a tall matrix, ti*BM.. of a wide one); at most 2^28 of them.
+        const int64_t cols = d.cols;
+        const int64_t base = tall ? int64_t(tj) * BN * cols + int64_t(ti) * BM : int64_t(ti) * BM * cols + int64_t(tj) * BN;
+        const int64_t span = (tall ? int64_t(BN - 1) : int64_t(BM - 1)) * cols + (tall ? BM : BN);
+        const int64_t avail = max(int64_t(0), min(span, d.rows * d.cols - base));
+        const int esz = bf ? 2 : 4;
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc(reinterpret_cast<const char*>(d.param) + base * esz, avail * esz);
+        auto where = [&](int it, int64_t& orow, int64_t& ocol, int64_t& cap, int64_t& left) {
+            if (tall) {
+                const int k = it * kGemmThreads + tid;
+                orow = int64_t(tj) * BN + k / NCH;
+                ocol = int64_t(ti) * BM + (k % NCH) * 8;
+                cap = orow < g.n ? 8 : 0;
+                left = g.m - ocol;
+            } else {
+                coords(it, orow, ocol);
+                cap = orow < g.m ? 8 : 0;
+                left = g.n - ocol;
+            }
+        };
+        auto value = [&](int it) {
+            if (tall) {
+                const int k = it * kGemmThreads + tid, x = k / NCH, c = k % NCH;
+                return *reinterpret_cast<const uint4*>(TT + x * BM + (((c ^ x ^ (x >> 3)) & (NCH - 1)) << 3));
+            }
+            int64_t orow, ocol;
+            return gather(it, orow, ocol);
+        };
+        // ntp: the tall path's non-temporal parameter accesses
+        auto run = [&](auto ntp) __attribute__((always_inline)) {
+            constexpr bool NTP = decltype(ntp)::value;
+            ApplyPiece pc[U];
+#pragma unroll
+            for (int i = 0; i < NREST; ++i) src_load(NPRE + wave * NREST + i);
+            // The parameter loads must follow the coefficient DMA in issue
+            // order (the wait below counts on it): nothing moves across this.
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                int64_t orow, ocol, cap, left;
+                where(u, orow, ocol, cap, left);
+                apply_begin_buf<NTP>(d, pc[u], orow, ocol, cap, left, rp, base);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            // The coefficient tile is complete once at most the U (bf16) or
+            // 2U (fp32) parameter loads issued after it remain.
+            if (bf)
+                __builtin_amdgcn_s_waitcnt(0x0070 | (U & 15) | ((U >> 4) << 14));
+            else
+                __builtin_amdgcn_s_waitcnt(0x0070 | ((2 * U) & 15) | (((2 * U) >> 4) << 14));
+            asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+            for (int a = 0; a < FM; ++a) combine_row(a);
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): the combined tile is in LDS
+            asm volatile("s_barrier" ::: "memory");
+#pragma unroll
+            for (int u = 0; u < U; ++u) pc[u].w = value(u);
+#pragma unroll
+            for (int u = 0; u < U; ++u) apply_end<NTP>(d, pc[u], g.keep);
+            for (int it0 = U; it0 < NT; it0 += U) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    int64_t orow, ocol, cap, left;
+                    where(it0 + u, orow, ocol, cap, left);
+                    apply_begin<NTP>(d, pc[u], orow, ocol, cap, left);
+                    pc[u].w = value(it0 + u);
+                }
+#pragma unroll
+                for (int u = 0; u < U; ++u) apply_end<NTP>(d, pc[u], g.keep);
+            }
+        };
+        if (tall)
+            run(std::true_type{});
+        else
+            run(std::false_type{});
+        return;
+    }
+
 #pragma unroll
     for (int a = 0; a < FM; ++a) combine_row(a);
     __syncthreads();
@@ -1265,52 +1386,12 @@ __global__ __launch_bounds__(kGemmThreads, BM == 128 ? 2 : 1) void ns_gemm_kerne
 
 
     if (has_tr) {
-        if constexpr (MODE == MODE_APPLY) {
-            // Parameter rows of a tall matrix, in batches of U pieces: all U
-            // parameter loads, then the U updates.  (Keeping the next batch's
-            // loads in flight while finishing one measured no faster: the
-            // parameter traffic of all CUs at once is what bounds this part.)
-            constexpr int U = NT % 8 == 0 ? 8 : 6;
-            static_assert(NT % U == 0, "whole batches");
-            for (int it0 = 0; it0 < NT; it0 += U) {
-                ApplyPiece pc[U];
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    const int k = (it0 + u) * kGemmThreads + tid;
-                    const int x = k / NCH, c = k % NCH;
-                    const int64_t orow = int64_t(tj) * BN + x, ocol = int64_t(ti) * BM + c * 8;
-                    apply_begin<true>(d, pc[u], orow, ocol, orow < g.n ? int64_t(8) : int64_t(0), g.m - ocol);
-                    pc[u].w = *reinterpret_cast<const uint4*>(TT + x * BM + (((c ^ x ^ (x >> 3)) & (NCH - 1)) << 3));
-                }
-#pragma unroll
-                for (int u = 0; u < U; ++u) apply_end<true>(d, pc[u], g.keep);
-            }
-        } else {
 #pragma unroll 8
-            for (int it = 0; it < NT; ++it) store_tr(it);
-        }
+        for (int it = 0; it < NT; ++it) store_tr(it);
     }
     if (has_dir) {
-        if constexpr (MODE == MODE_APPLY) {
-            // Parameter rows of a wide matrix, in batches of U pieces: all U
-            // parameter loads, then the U updates.
-            constexpr int U = NIT % 8 == 0 ? 8 : 6;
-            static_assert(NIT % U == 0, "whole batches");
-            for (int it0 = 0; it0 < NIT; it0 += U) {
-                ApplyPiece pc[U];
-#pragma unroll
-                for (int u = 0; u < U; ++u) {
-                    int64_t orow, ocol;
-                    pc[u].w = gather(it0 + u, orow, ocol);
-                    apply_begin(d, pc[u], orow, ocol, orow < g.m ? int64_t(8) : int64_t(0), g.n - ocol);
-                }
-#pragma unroll
-                for (int u = 0; u < U; ++u) apply_end(d, pc[u], g.keep);
-            }
-        } else {
 #pragma unroll 4
-            for (int it = 0; it < NIT; ++it) store_dir(it);
-        }
+        for (int it = 0; it < NIT; ++it) store_dir(it);
     }
 }
 
