@@ -672,6 +672,10 @@ def main():
     ap.add_argument("--calib-copy", action="store_true",
                     help="only copy 1 GiB three times (torch copy_): the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run")
+    ap.add_argument("--adamw-set", choices=["c2", "llama8b"],
+                    help="only the AdamW step on one tensor set (config 2, or the Llama-8B AdamW tensors: embedding, "
+                         "LM head, 65 norms), 6 steps with the memory-side cache flushed before each: the workload of "
+                         "the rocprofv3 memory-path counter runs")
     ap.add_argument("--gpt2-in-order", action="store_true",
                     help="only the GPT-2 (config 4) step with its Muon shape classes run in order (no side "
                          "streams), for a kernel trace whose per-kernel durations do not overlap")
@@ -695,6 +699,34 @@ def main():
             y.copy_(x)
         torch.cuda.synchronize()
         print(json.dumps({"calib_copy_bytes_each_way": x.numel() * 4, "copies": 3}), flush=True)
+        return
+    if args.adamw_set:
+        from helpers import c2_sizes
+        from triton_muon_adamw.adamw import HipAdamW
+
+        sizes = c2_sizes() if args.adamw_set == "c2" else [
+            int(torch.Size(s).numel()) for _, s, b in llama8b_layout() if b == "adam"]
+        gen = torch.Generator(device=dev).manual_seed(args.seed)
+        params = []
+        for n in sizes:
+            p = torch.nn.Parameter(torch.empty(n, device=dev).normal_(0.0, 0.02, generator=gen))
+            p.grad = torch.empty(n, device=dev).normal_(0.0, 1e-3, generator=gen)
+            params.append(p)
+        opt = HipAdamW(params, lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, eps=1e-8)
+        flush = torch.empty(1 << 27, device=dev)
+        ms = []
+        for _ in range(6):
+            flush.fill_(0.0)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            opt.step()
+            e1.record()
+            torch.cuda.synchronize()
+            ms.append(e0.elapsed_time(e1))
+        gbs = 28.0 * sum(sizes) / (statistics.median(ms[1:]) * 1e-3) / 1e9
+        print(json.dumps({"workload": f"AdamW step alone, {args.adamw_set} set", "elements": sum(sizes),
+                          "tensors": len(sizes), "step_ms_median": round(statistics.median(ms[1:]), 4),
+                          "GB/s": round(gbs, 1)}), flush=True)
         return
     if args.gpt2_in_order:
         from triton_muon_adamw import MuonAdamW

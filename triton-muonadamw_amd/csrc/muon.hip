@@ -1656,11 +1656,12 @@ int muon_step_impl(const mamw_muon_matrix* mats, int batch, double lr, double we
     const bool lower = kmajor && utile == p.tile && p.mp >= 2 * p.tile;
     // 128 x 192 update tiles (two workgroups per CU, 17% less operand traffic
     // per flop than 128 x 128) where the class runs 128 tiles throughout, n
-    // pads to a multiple of 192 and the grid holds at least two rounds of
+    // pads to a multiple of 192 and the grid holds at least 1.5 rounds of
     // 2 x 256 workgroups (GPT-2's 24 x 768 x 3072 class: update -6%, APPLY
-    // -7%; smaller grids leave CUs idle: 12 x 768 x 768 +22%).
+    // -7%; 12 x 768 x 2304, 864 tiles: update -2%; smaller grids leave CUs
+    // idle: 12 x 768 x 768, 288 tiles, +22%).
     const bool rect = utile == 128 && lower && p.np % 192 == 0 &&
-                      int64_t(batch) * (p.mp / 128) * (p.np / 192) >= 1024;
+                      int64_t(batch) * (p.mp / 128) * (p.np / 192) >= 768;
     const int ucode = rect ? kTile128x192 : utile;
     int cur = 0;
     for (int it = 0; it < ns_steps; ++it) {
