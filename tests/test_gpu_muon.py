@@ -455,3 +455,21 @@ def test_ns_exact_on_orthogonal_rows(gpu, count, shape):
             o.step()
         for q, (qs, _) in zip(params, singles):
             assert torch.equal(q.detach(), qs[0].detach())
+
+
+def test_side_streams_are_per_thread(gpu):
+    """The library's side streams are made once per calling thread and device:
+    the same thread gets the same streams again, another thread its own (a
+    graph capture on one thread forks its streams into the capture, so they
+    must not be shared with a thread stepping eagerly meanwhile)."""
+    import threading
+
+    from triton_muon_adamw import _lib
+    mine = [s.cuda_stream for s in _lib.side_streams(gpu, 2)]
+    assert [s.cuda_stream for s in _lib.side_streams(gpu, 2)] == mine
+    assert [s.cuda_stream for s in _lib.side_streams(gpu, 1)] == mine[:1]
+    other = []
+    t = threading.Thread(target=lambda: other.extend(s.cuda_stream for s in _lib.side_streams(gpu, 2)))
+    t.start()
+    t.join()
+    assert len(other) == 2 and not set(other) & set(mine)

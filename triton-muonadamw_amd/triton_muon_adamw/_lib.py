@@ -11,6 +11,7 @@ Status codes map to exceptions: negative (argument rejected on the host) ->
 from __future__ import annotations
 
 import ctypes
+import threading
 from ctypes import POINTER, c_char_p, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
@@ -197,13 +198,17 @@ def stream_handle(device: torch.device) -> int:
 
 
 _HIP_STREAM_NON_BLOCKING = 1
-_side_streams: dict[int, list] = {}
+_side_streams: dict[tuple[int, int], list] = {}
+_side_streams_lock = threading.Lock()
 
 
 def side_streams(device: torch.device, count: int) -> list:
     """``count`` streams of the library's own on ``device`` for shape classes
-    that run beside the caller's stream, made once per device and kept for the
-    life of the process.
+    that run beside the caller's stream, made once per calling thread and
+    device and kept for the life of the process.  Per thread: a thread that
+    captures a step into a graph forks these streams into the capture, so an
+    optimizer stepping eagerly on another thread must not queue work on the
+    same streams meanwhile.
 
     They come from hipStreamCreateWithFlags(hipStreamNonBlocking), looked up
     through this library's handle (so from the HIP runtime the library and
@@ -217,7 +222,8 @@ def side_streams(device: torch.device, count: int) -> list:
     idx = torch.device(device).index
     if idx is None:
         idx = torch.cuda.current_device()
-    have = _side_streams.setdefault(idx, [])
+    with _side_streams_lock:
+        have = _side_streams.setdefault((threading.get_ident(), idx), [])
     if len(have) < count:
         create = load().hipStreamCreateWithFlags
         create.restype = c_int
