@@ -86,3 +86,41 @@ def test_muon_bf16_vs_oracle(gpu, shape):
     # A bf16 parameter quantises the step: one ulp of p (~1.2e-4 at |p| ~ 0.02) is a quarter of a typical
     # update (adj * |u| ~ 5e-4), so elements whose update sits near a rounding boundary flip by one ulp.
     assert np.linalg.norm(u_got - u_ref) / np.linalg.norm(u_ref) < 5e-2
+
+
+@pytest.mark.parametrize("shapes,tile", [([(1024, 2048)] * 4 + [(2048, 1024)] * 4, 256),
+                                         ([(768, 3072)] * 6 + [(3072, 768)] * 6, 192)])
+def test_muon_bf16_params_batched_equal_single(gpu, shapes, tile):
+    """bf16 parameters through the batched APPLY epilogues of the 256 x 256
+    tile and of the 128 x 192 update tile (the group of 8 or 12) against each
+    matrix stepped alone (128 x 128 tiles): the same products in the same
+    order, so parameters and momenta agree bit for bit, both orientations."""
+    from triton_muon_adamw import _lib
+    gen = torch.Generator().manual_seed(13)
+    vals = [((torch.randn(s, generator=gen) * 0.02).bfloat16(), torch.randn(s, generator=gen).bfloat16(),
+             torch.randn(s, generator=gen) * 1e-3) for s in shapes]
+    kw = dict(lr=2e-2, weight_decay=0.1, coeffs=(3.4445, -4.7750, 2.0315), nesterov=True, beta=0.95, ns_steps=5,
+              eps=1e-7)
+
+    def make(p0, g0, m0):
+        p = torch.nn.Parameter(p0.to(gpu))
+        p.grad = g0.to(gpu)
+        return p
+
+    group = [make(*v) for v in vals]
+    opt = HipMuon(group, **kw)
+    for p, v in zip(group, vals):
+        opt.momentum[p].copy_(v[2].to(gpu))
+    _lib.prof_start()
+    opt.step()
+    _lib.prof_stop()
+    assert {r["variant"] // 8 for r in _lib.prof_collect() if r["kernel"] == "ns_gemm_kernel:apply"} == {tile}
+    for v, p in zip(vals, group):
+        q = make(*v)
+        o = HipMuon([q], **kw)
+        o.momentum[q].copy_(v[2].to(gpu))
+        o.step()
+        torch.cuda.synchronize()
+        assert q.dtype == torch.bfloat16
+        assert torch.equal(p.detach(), q.detach())
+        assert torch.equal(opt.momentum[p], o.momentum[q])
