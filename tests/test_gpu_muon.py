@@ -294,9 +294,12 @@ def test_concurrent_classes_equal_in_order(gpu, on_side_stream, classes):
 # Launch groups that exercise the tile and storage choices: two block rows
 # (m just above 128, lower-triangle A and B), ragged n, tall matrices, the
 # 256-wide tile from m = 1024 in groups of 8 or more (and the padding rule
-# that keeps the 128 tile), and m >= 2048.
+# that keeps the 128 tile), m >= 2048, and the 128 x 192 update tile on
+# ragged matrices.
 SWEEP = [(3, (200, 520)), (5, (700, 260)), (1, (129, 4000)), (8, (1024, 1300)), (9, (1100, 2100)),
-         (8, (1024, 2100)), (8, (1280, 2560)), (8, (4096, 1024)), (2, (2100, 2300))]
+         (8, (1024, 2100)), (8, (1280, 2560)), (8, (4096, 1024)), (2, (2100, 2300)),
+         # 128 x 192 update tiles over ragged edges (padded 768 x 768, 32 x 6 x 4 = 768 tiles), both orientations
+         (32, (700, 760)), (32, (760, 700))]
 
 
 @pytest.mark.parametrize("count,shape", SWEEP)
