@@ -3,8 +3,8 @@
 * Long horizon (muon_adamw_benchmark.py:99-134): the reference steps its
   hybrid optimizer and the torch wrapper many times on static gradients and
   then compares every parameter at atol = rtol = 1e-2.  Here: the
-  GPT-2-124M-shaped set (config 4), 150 static-gradient steps (one 50 + 100
-  loop of that script), this build against ``PyTorchMuonAdamW`` on the GPU.
+  GPT-2-124M-shaped set (config 4), 750 static-gradient steps (that script's
+  five 50 + 100 loops), this build against ``PyTorchMuonAdamW`` on the GPU.
 * ``parameter_split="auto"`` (optimizer.py:117-130, the reference's default)
   on an HF-style module: ``get_input_embeddings`` / ``get_output_embeddings``,
   a head tied to the embedding (deduplicated by ``data_ptr``), a frozen
@@ -52,9 +52,10 @@ def _split(named):
 
 
 def test_gpt2_long_horizon_static_gradients(gpu):
-    """150 steps on one fixed set of gradients, then every parameter within
-    atol = rtol = 1e-2 of the torch wrapper's (the reference's end check,
-    muon_adamw_benchmark.py:128-134), AdamW parameters within 1e-5."""
+    """750 steps on one fixed set of gradients (the reference's five rounds of
+    50 warm-up + 100 timed steps, muon_adamw_benchmark.py:99-124), then every
+    parameter within atol = rtol = 1e-2 of the torch wrapper's (its end check,
+    :128-134), AdamW parameters within 1e-5."""
     mc = _mc()
     gen = torch.Generator(device=gpu).manual_seed(3)
     mine, theirs = [], []
@@ -68,7 +69,7 @@ def test_gpt2_long_horizon_static_gradients(gpu):
     start = [p.detach().clone() for _, p, _ in mine]
     opt = MuonAdamW(_split(mine), muon_config=mc, adam_config=AC, parameter_split="explicit")
     ref = PyTorchMuonAdamW(_split(theirs), muon_config=mc, adam_config=AC, parameter_split="explicit")
-    for _ in range(150):
+    for _ in range(5 * (50 + 100)):
         opt.step()
         ref.step()
     torch.cuda.synchronize()
