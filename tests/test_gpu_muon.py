@@ -390,33 +390,34 @@ def test_config3_concurrent_step_vs_torch(gpu):
         assert err <= 1e-2, f"{tuple(p.shape)}: update rel err {err} against torch's Newton-Schulz"
 
 
-def _orthogonal_signs(rows, cols, rng):
+def _orthogonal_signs(rows, cols, rng, order=4096):
     """rows x cols, rows mutually orthogonal: distinct rows of the Sylvester
-    Hadamard matrix of order 4096 (entry (-1)^popcount(i & j)), with random
-    column signs, placed on 4096 random columns (zero elsewhere)."""
-    r = rng.choice(4096, size=rows, replace=False)
-    x = np.bitwise_and.outer(r, np.arange(4096))
+    Hadamard matrix of order `order` (entry (-1)^popcount(i & j)), with random
+    column signs, placed on `order` random columns (zero elsewhere)."""
+    r = rng.choice(order, size=rows, replace=False)
+    x = np.bitwise_and.outer(r, np.arange(order))
     pop = np.zeros_like(x)
     while x.any():
         pop += x & 1
         x >>= 1
-    h = np.where(pop & 1, -1.0, 1.0).astype(np.float32) * rng.choice([-1.0, 1.0], size=4096).astype(np.float32)
+    h = np.where(pop & 1, -1.0, 1.0).astype(np.float32) * rng.choice([-1.0, 1.0], size=order).astype(np.float32)
     out = np.zeros((rows, cols), np.float32)
-    out[:, rng.permutation(cols)[:4096]] = h
+    out[:, rng.permutation(cols)[:order]] = h
     return out
 
 
 
-@pytest.mark.parametrize("count,shape", [(16, (1024, 4096)), (1, (14336, 4096))])
-def test_ns_exact_on_orthogonal_rows(gpu, count, shape):
+@pytest.mark.parametrize("count,shape,order", [(16, (1024, 4096), 4096), (1, (14336, 4096), 4096),
+                                               (16, (512, 2304), 2048)])
+def test_ns_exact_on_orthogonal_rows(gpu, count, shape, order):
     """The whole Newton-Schulz pipeline on inputs where every product is exact
     in any summation order, so the result is known bit for bit.
 
     The gradients' rows (in the m x n orientation) are orthogonal +-1 vectors
-    with 4096 nonzeros; with zero momentum, beta = 0 and no Nesterov blend,
-    X0 = G / ||G||_F = +-2^-e exactly (||G||_F = 2^e), every Gram partial sum
-    is an integer multiple of 2^-2e below 2^24 of them, and A = X0 X0^T =
-    lam I with lam = 4096 * 2^-2e.  Coefficients (0, 1/lam, 0) make B = I and
+    with `order` nonzeros (4096 or 2048); with zero momentum, beta = 0 and no
+    Nesterov blend, X0 = G / ||G||_F = +-2^-e exactly (||G||_F^2 = m * order
+    = 2^2e), every Gram partial sum is an integer multiple of 2^-2e below 2^24
+    of them, and A = X0 X0^T = lam I with lam = order * 2^-2e.  Coefficients (0, 1/lam, 0) make B = I and
     every iterate X0 again, so with zero parameters the step writes
     -slr * X0 = -s G for one scalar s = slr * 2^-e.  A k block lost, doubled
     or summed into another tile, a block of A or B above the diagonal read
@@ -425,15 +426,19 @@ def test_ns_exact_on_orthogonal_rows(gpu, count, shape):
     an off-diagonal tile of A).  The 16 matrices of 1024 x 4096 run on
     256-wide tiles with lower-triangle A and B; each stepped alone (128-wide
     Gram and polynomial, mirrored A and B) gives the same bits.  The
-    14336 x 4096 matrix runs transposed."""
+    14336 x 4096 matrix runs transposed.  The 16 matrices of 512 x 2304 run
+    their updates on 128 x 192 tiles (768 of them); each alone on 128 x 128."""
+    from triton_muon_adamw import _lib
     rng = np.random.default_rng(17)
     m_, n_ = min(shape), max(shape)
     grads = []
     for _ in range(count):
-        x = _orthogonal_signs(m_, n_, rng)
+        x = _orthogonal_signs(m_, n_, rng, order)
         grads.append(torch.from_numpy(x if shape[0] <= shape[1] else np.ascontiguousarray(x.T)))
-    e = (int(np.log2(m_)) + 12) // 2  # ||G||_F^2 = m * 4096
-    lam = 4096.0 * 2.0 ** (-2 * e)
+    e2 = int(np.log2(m_)) + int(np.log2(order))  # ||G||_F^2 = m * order = 2^e2
+    assert m_ * order == 2 ** e2 and e2 % 2 == 0
+    e = e2 // 2
+    lam = order * 2.0 ** (-2 * e)
     coeffs = (0.0, 1.0 / lam, 0.0)
     lr = 2e-2
 
@@ -444,8 +449,13 @@ def test_ns_exact_on_orthogonal_rows(gpu, count, shape):
         return params, HipMuon(params, lr=lr, coeffs=coeffs, beta=0.0, nesterov=False, weight_decay=0.1)
 
     params, opt = make(grads)
+    _lib.prof_start()
     opt.step()
+    _lib.prof_stop()
     assert [c.n for c in opt._calls] == [count]
+    update_tiles = {r["variant"] // 8 for r in _lib.prof_collect() if r["kernel"] in ("ns_gemm_kernel:update",
+                                                                                     "ns_gemm_kernel:apply")}
+    assert update_tiles == ({192} if shape == (512, 2304) else {256})
     slr = scaled_lr(lr, "original", *shape)
     for i, (q, g) in enumerate(zip(params, grads)):
         got = q.detach().cpu()
