@@ -31,6 +31,8 @@ CPU over a bounded sample of the same workload: the GPU run's own layer-0
 values, copied to the host before the first step.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
+       (single-workload modes for profiling: --calib-copy, --adamw-set c2|llama8b, --muon-group BxRxC,
+       --gpt2-in-order)
 """
 
 from __future__ import annotations
@@ -676,6 +678,10 @@ def main():
                     help="only the AdamW step on one tensor set (config 2, or the Llama-8B AdamW tensors: embedding, "
                          "LM head, 65 norms), 6 steps with the memory-side cache flushed before each: the workload of "
                          "the rocprofv3 memory-path counter runs")
+    ap.add_argument("--muon-group", metavar="BxRxC",
+                    help="only the Muon step of one launch group of B matrices R x C (N(0,0.02) parameters, "
+                         "N(0,1e-3) gradients), --steps timed after --warmup: the workload of the per-kernel "
+                         "counter runs on single shape classes")
     ap.add_argument("--gpt2-in-order", action="store_true",
                     help="only the GPT-2 (config 4) step with its Muon shape classes run in order (no side "
                          "streams), for a kernel trace whose per-kernel durations do not overlap")
@@ -727,6 +733,23 @@ def main():
         print(json.dumps({"workload": f"AdamW step alone, {args.adamw_set} set", "elements": sum(sizes),
                           "tensors": len(sizes), "step_ms_median": round(statistics.median(ms[1:]), 4),
                           "GB/s": round(gbs, 1)}), flush=True)
+        return
+    if args.muon_group:
+        from triton_muon_adamw.muon import HipMuon
+
+        count, rows, cols = (int(v) for v in args.muon_group.split("x"))
+        gen = torch.Generator(device=dev).manual_seed(args.seed)
+        params = []
+        for _ in range(count):
+            p = torch.nn.Parameter(torch.empty((rows, cols), device=dev).normal_(0.0, 0.02, generator=gen))
+            p.grad = torch.empty((rows, cols), device=dev).normal_(0.0, 1e-3, generator=gen)
+            params.append(p)
+        mc, _ = configs()
+        opt = HipMuon(params, lr=mc.lr, weight_decay=mc.weight_decay, coeffs=mc.coeffs, nesterov=True, beta=0.95,
+                      ns_steps=5, eps=mc.eps)
+        ms, wall, _ = time_steps(opt, args.steps, args.warmup)
+        print(json.dumps({"workload": f"Muon step of {count} x {rows}x{cols}", "groups": [c.n for c in opt._calls],
+                          "ms_per_step": round(ms, 4), "steps": args.steps, "warmup": args.warmup}), flush=True)
         return
     if args.gpt2_in_order:
         from triton_muon_adamw import MuonAdamW
