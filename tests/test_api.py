@@ -359,3 +359,35 @@ def test_concurrent_class_lanes_one_class_per_device(monkeypatch):
              hip_muon._Call("d1", None, 1, 0, 2048, 4096, 2)]
     lanes, _ = hip_muon._lanes(calls, 5, {"d0": 256, "d1": 256})
     assert lanes[("d0", 0)] is None and lanes[("d1", 2)] is None and lanes[("d1", 1)] == "d1/s0"
+
+
+def test_side_streams_of_ended_threads_are_reused():
+    """A thread's side streams go back to a free list when it ends and the
+    next thread takes them from there (stand-in objects for the streams, a
+    device index no GPU has: nothing here calls HIP)."""
+    import gc
+    import threading
+
+    from triton_muon_adamw import _lib
+
+    dev = torch.device("cuda", 97)
+
+    def first():
+        _lib._thread_side_streams.streams = _lib._ThreadStreams()
+        _lib._thread_side_streams.streams.by_device[97] = ["s0", "s1"]
+
+    t = threading.Thread(target=first)
+    t.start()
+    t.join()
+    gc.collect()
+    try:
+        assert sorted(_lib._free_side_streams.get(97, [])) == ["s0", "s1"]
+        got = []
+        t = threading.Thread(target=lambda: got.extend(_lib.side_streams(dev, 2)))
+        t.start()
+        t.join()
+        gc.collect()
+        assert sorted(got) == ["s0", "s1"]
+        assert sorted(_lib._free_side_streams.get(97, [])) == ["s0", "s1"]  # returned again
+    finally:
+        _lib._free_side_streams.pop(97, None)

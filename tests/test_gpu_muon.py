@@ -474,7 +474,9 @@ def test_side_streams_are_per_thread(gpu):
     """The library's side streams are made once per calling thread and device:
     the same thread gets the same streams again, another thread its own (a
     graph capture on one thread forks its streams into the capture, so they
-    must not be shared with a thread stepping eagerly meanwhile)."""
+    must not be shared with a thread stepping eagerly meanwhile); a thread
+    that ends hands its streams on to the next thread."""
+    import gc
     import threading
 
     from triton_muon_adamw import _lib
@@ -486,3 +488,10 @@ def test_side_streams_are_per_thread(gpu):
     t.start()
     t.join()
     assert len(other) == 2 and not set(other) & set(mine)
+    # the ended thread's streams go to the next thread instead of new ones
+    gc.collect()
+    later = []
+    t = threading.Thread(target=lambda: later.extend(s.cuda_stream for s in _lib.side_streams(gpu, 2)))
+    t.start()
+    t.join()
+    assert set(later) == set(other)

@@ -198,17 +198,34 @@ def stream_handle(device: torch.device) -> int:
 
 
 _HIP_STREAM_NON_BLOCKING = 1
-_side_streams: dict[tuple[int, int], list] = {}
+# Streams of threads that have exited, per device index, for reuse by new threads.
+_free_side_streams: dict[int, list] = {}
 _side_streams_lock = threading.Lock()
+_thread_side_streams = threading.local()
+
+
+class _ThreadStreams:
+    """One thread's side streams per device; when the thread ends (its
+    thread-local storage is released) they return to the free list."""
+
+    def __init__(self):
+        self.by_device: dict[int, list] = {}
+
+    def __del__(self):
+        with _side_streams_lock:
+            for idx, streams in self.by_device.items():
+                _free_side_streams.setdefault(idx, []).extend(streams)
 
 
 def side_streams(device: torch.device, count: int) -> list:
     """``count`` streams of the library's own on ``device`` for shape classes
-    that run beside the caller's stream, made once per calling thread and
-    device and kept for the life of the process.  Per thread: a thread that
-    captures a step into a graph forks these streams into the capture, so an
-    optimizer stepping eagerly on another thread must not queue work on the
-    same streams meanwhile.
+    that run beside the caller's stream, per calling thread and device.  Per
+    thread: a thread that captures a step into a graph forks these streams
+    into the capture, so an optimizer stepping eagerly on another thread must
+    not queue work on the same streams meanwhile.  A thread's streams are
+    created on first use and go back to a free list when the thread ends, for
+    the next thread to take (none is destroyed: at most as many exist as
+    threads have used them at once).
 
     They come from hipStreamCreateWithFlags(hipStreamNonBlocking), looked up
     through this library's handle (so from the HIP runtime the library and
@@ -222,8 +239,15 @@ def side_streams(device: torch.device, count: int) -> list:
     idx = torch.device(device).index
     if idx is None:
         idx = torch.cuda.current_device()
-    with _side_streams_lock:
-        have = _side_streams.setdefault((threading.get_ident(), idx), [])
+    mine = getattr(_thread_side_streams, "streams", None)
+    if mine is None:
+        mine = _thread_side_streams.streams = _ThreadStreams()
+    have = mine.by_device.setdefault(idx, [])
+    if len(have) < count:
+        with _side_streams_lock:
+            free = _free_side_streams.get(idx, [])
+            while free and len(have) < count:
+                have.append(free.pop())
     if len(have) < count:
         create = load().hipStreamCreateWithFlags
         create.restype = c_int
