@@ -558,10 +558,16 @@ def bench_vs_torch_gpu(dev, seed: int = 0):
       times it, compiled by torch.compile (inductor); warm-up 50, 100 timed
       steps, mean of 5 loops (:99-126).  Published: 1.24-1.26x against the
       compiled step (README.md:48).
+    * ref_muon_mlp: the reference's Muon benchmark model (five bias-free
+      linear layers, muon_benchmark.py:14-24, all to Muon), HipMuon against
+      torch.optim.Muon with the reference's settings (:33-35), eager and
+      compiled; warm-up 50, 100 timed steps, mean of 5 loops (:66-92).
+      Published: 1.33-1.35x eager, 1.27-1.30x compiled (README.md:46-47).
     * ref_adamw_mlp: the reference's AdamW benchmark model
-      (adam_benchmark.py:14-25,33-42), HipAdamW against fused torch AdamW;
-      warm-up 100, 500 timed steps, mean of 10 loops (:75-108).  Published:
-      0.97-0.99x (README.md:45).
+      (adam_benchmark.py:14-25,33-42), HipAdamW against fused torch AdamW
+      and against torch's default (foreach) AdamW; warm-up 100, 500 timed
+      steps, mean of 10 loops (:75-108).  Published: 0.97-0.99x against the
+      fused and 2.65-2.70x against the foreach step (README.md:44-45).
     * gpt2, llama_layer (layer 0 plus 1/32 of the embedding and LM head),
       c2_adamw: the BASELINE configurations, shorter loops.
     """
@@ -627,16 +633,44 @@ def bench_vs_torch_gpu(dev, seed: int = 0):
         r["compiled_torch_error"] = f"{type(e).__name__}: {str(e)[:200]}"
     out["ref_hybrid_mlp"] = r
     log(f"[vs torch gpu] reference hybrid MLP: {r}")
+    del mine, ref, a, b
+    # reference Muon benchmark (muon_benchmark.py:14-24,33-35)
+    from triton_muon_adamw.muon import HipMuon
+
+    dims = [1024, 2048, 4096, 4096, 4096, 1024]
+    a, b = twin([((fo, fi), "muon", normal(fi ** -0.5)) for fi, fo in zip(dims[:-1], dims[1:])])
+    mine = HipMuon(a["muon"], coeffs=(3.4445, -4.775, 2.0315), beta=0.95, lr=1e-3, weight_decay=0.1, ns_steps=5)
+    ref = torch.optim.Muon(b["muon"], lr=1e-3, momentum=0.95, nesterov=True, ns_steps=5)
+    mine_ms = event_loop_ms(mine.step, 50, 100, 5)
+    r = ratio(mine_ms, event_loop_ms(ref.step, 50, 100, 5))
+    r["published_speedup"] = "1.33-1.35 (vs torch.optim.Muon), 1.27-1.30 (vs its torch.compile'd step)"
+    try:
+        compiled = torch.compile(ref.step)
+        compiled()
+        torch.cuda.synchronize(dev)
+        c_ms = event_loop_ms(compiled, 50, 100, 5)
+        r["compiled_torch_ms"] = round(c_ms, 4)
+        r["speedup_vs_compiled"] = round(c_ms / mine_ms, 3)
+    except Exception as e:  # inductor is optional: record why the compiled point is missing
+        r["compiled_torch_error"] = f"{type(e).__name__}: {str(e)[:200]}"
+    out["ref_muon_mlp"] = r
+    log(f"[vs torch gpu] reference Muon MLP: {r}")
+    del mine, ref, a, b
     # reference AdamW benchmark (adam_benchmark.py:33-42)
     a, b = twin(mlp_shapes([1024, 4096, 4096, 4096, 1024]))
     pa, pb = a["adam"] + a["muon"], b["adam"] + b["muon"]
     mine = HipAdamW(pa, lr=1e-3, betas=(0.9, 0.999), weight_decay=1e-4, eps=1e-8)
     ref = torch.optim.AdamW(pb, lr=1e-3, betas=(0.9, 0.999), weight_decay=1e-4, eps=1e-8, fused=True)
-    r = ratio(event_loop_ms(mine.step, 100, 500, 10), event_loop_ms(ref.step, 100, 500, 10))
-    r["published_speedup"] = "0.97-0.99 (vs fused torch AdamW)"
+    mine_ms = event_loop_ms(mine.step, 100, 500, 10)
+    r = ratio(mine_ms, event_loop_ms(ref.step, 100, 500, 10))
+    r["published_speedup"] = "0.97-0.99 (vs fused torch AdamW), 2.65-2.70 (vs foreach AdamW)"
+    ref_fe = torch.optim.AdamW(pb, lr=1e-3, betas=(0.9, 0.999), weight_decay=1e-4, eps=1e-8, foreach=True)
+    fe_ms = event_loop_ms(ref_fe.step, 100, 500, 10)
+    r["foreach_torch_ms"] = round(fe_ms, 4)
+    r["speedup_vs_foreach"] = round(fe_ms / mine_ms, 3)
     out["ref_adamw_mlp"] = r
     log(f"[vs torch gpu] reference AdamW MLP: {r}")
-    del mine, ref, a, b, pa, pb
+    del mine, ref, ref_fe, a, b, pa, pb
     # BASELINE configurations
     mc, ac = configs()
     for name, layout in (("gpt2", gpt2_layout()),

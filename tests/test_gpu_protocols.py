@@ -5,6 +5,9 @@
   then compares every parameter at atol = rtol = 1e-2.  Here: the
   GPT-2-124M-shaped set (config 4), 750 static-gradient steps (that script's
   five 50 + 100 loops), this build against ``PyTorchMuonAdamW`` on the GPU.
+* The reference's Muon benchmark end check (muon_benchmark.py:95-101): its
+  five-layer model, 750 static-gradient steps of this build's Muon against
+  ``torch.optim.Muon``, every parameter at atol = rtol = 1e-2.
 * ``parameter_split="auto"`` (optimizer.py:117-130, the reference's default)
   on an HF-style module: ``get_input_embeddings`` / ``get_output_embeddings``,
   a head tied to the embedding (deduplicated by ``data_ptr``), a frozen
@@ -84,6 +87,37 @@ def test_gpt2_long_horizon_static_gradients(gpu):
             moved = ((p.detach() - p0).norm() / p0.norm()).item()
             diff = ((p.detach() - q.detach()).norm() / p0.norm()).item()
             assert moved > 20 * diff, (name, moved, diff)
+
+
+def test_muon_mlp_long_horizon_against_torch_muon(gpu):
+    """The reference's Muon benchmark end check (muon_benchmark.py:14-35,
+    50-60, 95-101): five bias-free linear layers, gradients from one MSE
+    backward pass on random data, then 5 x (50 + 100) steps of this build's
+    Muon and of torch.optim.Muon with the reference's settings; every
+    parameter within atol = rtol = 1e-2, and each matrix moved at least 20x
+    more than it differs from torch's."""
+    torch.manual_seed(5)
+    model = nn.Sequential(nn.Linear(1024, 2048, bias=False), nn.ReLU(), nn.Linear(2048, 4096, bias=False),
+                          nn.ReLU(), nn.Linear(4096, 4096, bias=False), nn.ReLU(),
+                          nn.Linear(4096, 4096, bias=False), nn.ReLU(), nn.Linear(4096, 1024, bias=False)).to(gpu)
+    twin = copy.deepcopy(model)
+    x = torch.randn(1000, 1024, device=gpu)
+    y = torch.randn(1000, 1024, device=gpu)
+    for m in (model, twin):
+        torch.nn.functional.mse_loss(m(x), y).backward()
+    start = [p.detach().clone() for p in model.parameters()]
+    mine = HipMuon(model.parameters(), coeffs=(3.4445, -4.775, 2.0315), beta=0.95, lr=1e-3, weight_decay=0.1,
+                   ns_steps=5)
+    ref = torch.optim.Muon(twin.parameters(), lr=1e-3, momentum=0.95, nesterov=True, ns_steps=5)
+    for _ in range(5 * (50 + 100)):
+        mine.step()
+        ref.step()
+    torch.cuda.synchronize()
+    for (name, p), q, p0 in zip(model.named_parameters(), twin.parameters(), start):
+        torch.testing.assert_close(p.detach(), q.detach(), atol=1e-2, rtol=1e-2, msg=name)
+        moved = ((p.detach() - p0).norm() / p0.norm()).item()
+        diff = ((p.detach() - q.detach()).norm() / p0.norm()).item()
+        assert moved > 20 * diff, (name, moved, diff)
 
 
 class _TinyLM(nn.Module):

@@ -211,10 +211,12 @@ class _ThreadStreams:
     def __init__(self):
         self.by_device: dict[int, list] = {}
 
-    def __del__(self):
-        with _side_streams_lock:
+    # The lock and the free list are bound as defaults: at interpreter exit
+    # the main thread's storage can outlive the module's globals.
+    def __del__(self, _lock=_side_streams_lock, _free=_free_side_streams):
+        with _lock:
             for idx, streams in self.by_device.items():
-                _free_side_streams.setdefault(idx, []).extend(streams)
+                _free.setdefault(idx, []).extend(streams)
 
 
 def side_streams(device: torch.device, count: int) -> list:
