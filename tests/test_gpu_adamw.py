@@ -4,7 +4,11 @@
   of triton_adam.py:53-59) over ragged sizes, unaligned views and
   several steps;
 * within the reference tolerance (atol 1e-4, rtol 1e-3; adam_benchmark.py:114)
-  of fused torch.optim.AdamW on the config 2 workload.
+  of fused torch.optim.AdamW on the config 2 workload;
+* the reference's own end check (adam_benchmark.py:14-43,57-62,75-114): its
+  LayerNorm MLP, gradients from one MSE backward pass, 10 x (100 + 500)
+  static-gradient steps against torch.optim.AdamW (its default, foreach),
+  every parameter within that tolerance.
 """
 
 import numpy as np
@@ -131,3 +135,33 @@ def test_adamw_config2_vs_torch_fused(gpu):
         worst = max(worst, (a.detach() - b.detach()).abs().max().item())
     # the two formulas differ only in rounding: far inside the reference tolerance
     assert worst < 1e-7, worst
+
+
+def test_adamw_mlp_long_horizon_against_torch(gpu):
+    """The reference's AdamW benchmark model and end check: 6000 steps of this
+    build's AdamW and of torch.optim.AdamW (foreach, as the reference runs it
+    by default) on the same static gradients, then every parameter within
+    atol = 1e-4, rtol = 1e-3 of torch's, and every parameter moved."""
+    import copy
+
+    import torch.nn as nn
+
+    torch.manual_seed(6)
+    model = nn.Sequential(nn.Linear(1024, 4096), nn.LayerNorm(4096), nn.ReLU(), nn.Linear(4096, 4096),
+                          nn.LayerNorm(4096), nn.ReLU(), nn.Linear(4096, 4096), nn.LayerNorm(4096), nn.ReLU(),
+                          nn.Linear(4096, 1024)).to(gpu)
+    twin = copy.deepcopy(model)
+    x = torch.randn(1000, 1024, device=gpu)
+    y = torch.randn(1000, 1024, device=gpu)
+    for m in (model, twin):
+        torch.nn.functional.mse_loss(m(x), y).backward()
+    start = [p.detach().clone() for p in model.parameters()]
+    mine = HipAdamW(model.parameters(), betas=(0.9, 0.999), lr=1e-3, weight_decay=1e-4, eps=1e-8)
+    ref = torch.optim.AdamW(twin.parameters(), lr=1e-3, betas=(0.9, 0.999), weight_decay=1e-4, eps=1e-8)
+    for _ in range(10 * (100 + 500)):
+        mine.step()
+        ref.step()
+    torch.cuda.synchronize()
+    for (name, p), q, p0 in zip(model.named_parameters(), twin.parameters(), start):
+        torch.testing.assert_close(p.detach(), q.detach(), atol=1e-4, rtol=1e-3, msg=name)
+        assert not torch.equal(p.detach(), p0), name
