@@ -5,6 +5,8 @@
   then compares every parameter at atol = rtol = 1e-2.  Here: the
   GPT-2-124M-shaped set (config 4), 750 static-gradient steps (that script's
   five 50 + 100 loops), this build against ``PyTorchMuonAdamW`` on the GPU.
+* The reference's hybrid benchmark end check on its own model and configs
+  (muon_adamw_benchmark.py:9-65,128-134), 750 static-gradient steps.
 * The reference's Muon benchmark end check (muon_benchmark.py:95-101): its
   five-layer model, 750 static-gradient steps of this build's Muon against
   ``torch.optim.Muon``, every parameter at atol = rtol = 1e-2.
@@ -84,6 +86,48 @@ def test_gpt2_long_horizon_static_gradients(gpu):
         else:
             # not vacuous: each matrix moved (relative Frobenius) at least 20x more
             # than it differs from the torch wrapper's
+            moved = ((p.detach() - p0).norm() / p0.norm()).item()
+            diff = ((p.detach() - q.detach()).norm() / p0.norm()).item()
+            assert moved > 20 * diff, (name, moved, diff)
+
+
+def test_hybrid_mlp_long_horizon_against_torch_wrapper(gpu):
+    """The reference's hybrid benchmark itself (muon_adamw_benchmark.py:9-65,
+    84-134): its LayerNorm MLP and configs, 2-D weights to Muon and the rest to
+    AdamW, gradients from one MSE backward pass, 5 x (50 + 100) steps of this
+    build and of PyTorchMuonAdamW; every parameter within atol = rtol = 1e-2,
+    the AdamW ones within the AdamW tolerance (atol 1e-4, rtol 1e-3,
+    adam_benchmark.py:114), and each Muon matrix moved at least 20x more than
+    it differs from the wrapper's."""
+    torch.manual_seed(4)
+    model = nn.Sequential(nn.Linear(1024, 2048), nn.LayerNorm(2048), nn.ReLU(), nn.Linear(2048, 4096),
+                          nn.LayerNorm(4096), nn.ReLU(), nn.Linear(4096, 4096), nn.LayerNorm(4096), nn.ReLU(),
+                          nn.Linear(4096, 1024)).to(gpu)
+    twin = copy.deepcopy(model)
+    x = torch.randn(1000, 1024, device=gpu)
+    y = torch.randn(1000, 1024, device=gpu)
+    for m in (model, twin):
+        torch.nn.functional.mse_loss(m(x), y).backward()
+    ac = AdamConfig(lr=1e-3, betas=(0.9, 0.999), eps=1e-7, weight_decay=0.01)
+    mc = MuonConfig(lr=1e-3, beta=0.95, eps=1e-7, weight_decay=0.1, coeffs=(3.445, -4.775, 2.0315), nesterov=True,
+                    ns_steps=5, adjust_lr_fn="original")
+
+    def split(m):
+        ps = [p for p in m.parameters() if p.requires_grad]
+        return {"adam": [p for p in ps if p.ndim != 2], "muon": [p for p in ps if p.ndim == 2]}
+
+    start = [p.detach().clone() for p in model.parameters()]
+    mine = MuonAdamW(split(model), muon_config=mc, adam_config=ac, parameter_split="explicit")
+    ref = PyTorchMuonAdamW(split(twin), muon_config=mc, adam_config=ac, parameter_split="explicit")
+    for _ in range(5 * (50 + 100)):
+        mine.step()
+        ref.step()
+    torch.cuda.synchronize()
+    for (name, p), q, p0 in zip(model.named_parameters(), twin.parameters(), start):
+        torch.testing.assert_close(p.detach(), q.detach(), atol=1e-2, rtol=1e-2, msg=name)
+        if p.ndim != 2:
+            torch.testing.assert_close(p.detach(), q.detach(), atol=1e-4, rtol=1e-3, msg=name)
+        else:
             moved = ((p.detach() - p0).norm() / p0.norm()).item()
             diff = ((p.detach() - q.detach()).norm() / p0.norm()).item()
             assert moved > 20 * diff, (name, moved, diff)
