@@ -330,6 +330,39 @@ def test_group_sweep_vs_torch(gpu, count, shape):
         assert err <= 1e-2, f"{count} x {shape}: update rel err {err} against torch's Newton-Schulz"
 
 
+@pytest.mark.parametrize("shape", [(200, 520), (520, 200)])
+def test_zero_gradient_members_only_decay(gpu, shape):
+    """A launch group whose members 1 and 3 have zero gradient and zero
+    momentum: X = 0, so ||X|| = 0 and X / max(||X||, eps) = 0 (torch's
+    clamp), the Newton-Schulz iterate stays 0 and the parameter only decays,
+    p * (1 - lr * wd) bit for bit as torch computes it; the momentum stays 0.
+    The other members, in the same launches, match torch's Newton-Schulz."""
+    from torch.optim._muon import _zeropower_via_newtonschulz
+    lr, wd, zero = 2e-2, 0.1, (1, 3)
+    ps, gs, ms, params, opt = _run_muon([shape] * 5, gpu, seed=13, lr=lr, weight_decay=wd)
+    for i in zero:
+        params[i].grad.zero_()
+        opt.momentum[params[i]].zero_()
+    mom0 = [opt.momentum[p].clone() for p in params]
+    opt.step()
+    torch.cuda.synchronize()
+    assert [c.n for c in opt._calls] == [5]
+    keep = 1 - lr * wd
+    slr = scaled_lr(lr, "original", *shape)
+    for i, (p0, p, g, m0) in enumerate(zip(ps, params, gs, mom0)):
+        p0 = p0.to(gpu)
+        if i in zero:
+            assert torch.equal(p.detach(), p0 * keep), f"member {i}: not a pure decay"
+            assert not opt.momentum[p].any()
+            continue
+        g = g.to(gpu)
+        mom = m0.lerp(g, 1 - 0.95)
+        ref = _zeropower_via_newtonschulz(g.lerp(mom, 0.95), COEFFS, 5, 1e-7).double()
+        u = (p0.double() * keep - p.detach().double()) / slr
+        err = ((u - ref).norm() / ref.norm()).item()
+        assert err <= 1e-2, f"member {i}: update rel err {err} against torch's Newton-Schulz"
+
+
 @pytest.mark.parametrize("shape", [(768, 3072), (1024, 4096), (4096, 4096), (14336, 4096)])
 def test_config3_ns_vs_torch(gpu, shape):
     """Config 3 shapes: blend momentum (beta 0.95, Nesterov), NS in bf16 vs torch's routine on the GPU."""
