@@ -100,6 +100,14 @@ def test_muonadamw_attributes_and_state_dict():
     opt.load_state_dict({"muon": new})
     assert opt.muon.model_params is new and opt.param_group["muon"] is new
     assert opt.param_groups[1]["params"] is new
+    # a parameter that joined a branch that way gets zero state on first use
+    mom = opt.state_dict()["muon"]["state"][0]["momentum_buffer"]
+    assert mom.shape == (2, 2) and mom.dtype == torch.float32 and not mom.any()
+    new_a = [nn.Parameter(torch.zeros(3))]
+    opt.load_state_dict({"adam": new_a})
+    opt.adamw.step_num = 1  # state_dict lists the moments only after a step, as torch does
+    st = opt.state_dict()["adam"]["state"][0]
+    assert st["exp_avg"].shape == (3,) and not st["exp_avg"].any() and not st["exp_avg_sq"].any()
     # state shapes: fp32 moments for AdamW, parameter-shaped momentum for Muon
     for p in opt.adamw.model_params:
         assert opt.adamw.m[p].shape == p.shape and opt.adamw.m[p].dtype == torch.float32
@@ -110,6 +118,15 @@ def test_muonadamw_attributes_and_state_dict():
 def test_invalid_adjust_lr_fn_raises_assertion():
     with pytest.raises(AssertionError, match="Invalid adjust_lr_fn"):
         MuonAdamW(TinyLM(), MuonConfig(adjust_lr_fn="bogus"))
+    # also when set through param_groups (checked before anything runs), where
+    # torch's None stands for "original"
+    opt = MuonAdamW(TinyLM())
+    opt.param_groups[1]["adjust_lr_fn"] = None
+    opt._pull_groups()
+    assert opt.muon.adjust_lr_fn == "original"
+    opt.param_groups[1]["adjust_lr_fn"] = "bogus"
+    with pytest.raises(AssertionError, match="Invalid adjust_lr_fn"):
+        opt.step()
 
 
 def test_zero_grad_zero_fills():

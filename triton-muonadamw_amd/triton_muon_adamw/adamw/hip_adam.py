@@ -127,10 +127,19 @@ class HipAdamW:
         self.m = {}
         self.v = {}
         for param in self.model_params:
-            self.m[param] = torch.zeros_like(param, dtype=torch.float32)
-            self.v[param] = torch.zeros_like(param, dtype=torch.float32)
+            self._moments(param)
         self._plan_key = None
         self._plans: list[_DevicePlan] = []
+
+    def _moments(self, param: nn.Parameter) -> tuple[torch.Tensor, torch.Tensor]:
+        """``(exp_avg, exp_avg_sq)`` of ``param``, created (zero, fp32) on first
+        use: at construction, or for a parameter that joined ``model_params``
+        later (a parameter list loaded in the reference's state format)."""
+        m = self.m.get(param)
+        if m is None:
+            m = self.m[param] = torch.zeros_like(param, dtype=torch.float32)
+            self.v[param] = torch.zeros_like(param, dtype=torch.float32)
+        return m, self.v[param]
 
     def _build_plans(self, active: list[nn.Parameter]) -> None:
         by_dev: dict[torch.device, list] = {}
@@ -140,7 +149,7 @@ class HipAdamW:
             _check_tensor(g, "param.grad", bf16_ok=True)
             if g.shape != p.shape or g.device != p.device:
                 raise ValueError("param.grad must match the parameter's shape and device")
-            m, v = self.m[p], self.v[p]
+            m, v = self._moments(p)
             _check_tensor(m, "exp_avg")
             _check_tensor(v, "exp_avg_sq")
             by_dev.setdefault(p.device, []).append((p, g, m, v))
@@ -264,8 +273,8 @@ class HipAdamW:
         state = {}
         if self.step_num > 0:
             for i, p in enumerate(self.model_params):
-                state[i] = {"step": torch.tensor(float(self.step_num)), "exp_avg": self.m[p],
-                            "exp_avg_sq": self.v[p]}
+                m, v = self._moments(p)
+                state[i] = {"step": torch.tensor(float(self.step_num)), "exp_avg": m, "exp_avg_sq": v}
         group = {"lr": self.lr, "betas": (self.beta1, self.beta2), "eps": self.eps,
                  "weight_decay": self.weight_decay, "amsgrad": False, "maximize": False, "foreach": None,
                  "capturable": self.capturable, "differentiable": False, "fused": True, "decoupled_weight_decay": True,
@@ -293,12 +302,12 @@ class HipAdamW:
             raise ValueError(f"per-parameter steps differ ({sorted(steps)}); this optimizer keeps one step counter")
         with torch.no_grad():
             for p in self.model_params:
-                self.m[p].zero_()
-                self.v[p].zero_()
+                for t in self._moments(p):
+                    t.zero_()
             for pid, st in state_dict["state"].items():
-                p = self.model_params[pos[pid]]
-                self.m[p].copy_(st["exp_avg"])
-                self.v[p].copy_(st["exp_avg_sq"])
+                m, v = self._moments(self.model_params[pos[pid]])
+                m.copy_(st["exp_avg"])
+                v.copy_(st["exp_avg_sq"])
         self.step_num = int(steps.pop()) if steps else 0
         lr, betas, eps, wd = hyper.pop() if hyper else (self.lr, (self.beta1, self.beta2), self.eps, self.weight_decay)
         self.lr, self.beta1, self.beta2, self.eps, self.weight_decay = lr, betas[0], betas[1], eps, wd

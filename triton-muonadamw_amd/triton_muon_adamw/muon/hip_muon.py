@@ -390,14 +390,24 @@ class HipMuon:
         self.eps = eps
         self.momentum = {}
         for param in self.model_params:
-            # fp32 state also for bf16 parameters (the reference uses the parameter's dtype, :407-412)
-            self.momentum[param] = torch.zeros_like(param, device=param.device, dtype=torch.float32)
+            self._momentum(param)
         self._plan_key = None
         self._plan_lr = lr
         self._calls: list[_Call] = []
         self._ws: dict = {}  # device (in order) or (device, shape class) (concurrent) -> workspace
         self._concurrent = False
         self._lanes: dict = {}  # (device, shape class) -> side stream, or None: the caller's stream
+
+    def _momentum(self, param: nn.Parameter) -> torch.Tensor:
+        """The momentum buffer of ``param``, created (zero) on first use: at
+        construction, or for a parameter that joined ``model_params`` later
+        (a parameter list loaded in the reference's state format).  fp32 also
+        for bf16 parameters (the reference uses the parameter's dtype,
+        :407-412)."""
+        buf = self.momentum.get(param)
+        if buf is None:
+            buf = self.momentum[param] = torch.zeros_like(param, device=param.device, dtype=torch.float32)
+        return buf
 
     def _build_calls(self, active: list[nn.Parameter]) -> None:
         groups: dict[tuple, list[nn.Parameter]] = {}
@@ -409,7 +419,7 @@ class HipMuon:
             _check_matrix(g, "param.grad", bf16_ok=True)
             if g.shape != p.shape or g.device != p.device:
                 raise ValueError("param.grad must match the parameter's shape and device")
-            _check_matrix(self.momentum[p], "momentum")
+            _check_matrix(self._momentum(p), "momentum")
             R, C = p.shape
             groups.setdefault((p.device, min(R, C), max(R, C)), []).append(p)
         calls = []
@@ -565,7 +575,7 @@ class HipMuon:
         returned by reference; one param group with this branch's
         hyperparameters (``adjust_lr_fn`` ``"original"`` written as torch's
         ``None``)."""
-        state = {i: {"momentum_buffer": self.momentum[p]} for i, p in enumerate(self.model_params)}
+        state = {i: {"momentum_buffer": self._momentum(p)} for i, p in enumerate(self.model_params)}
         group = {"lr": self.lr, "weight_decay": self.weight_decay, "momentum": self.beta,
                  "nesterov": self.is_nesterov, "ns_coefficients": (self.a, self.b, self.c), "eps": self.eps,
                  "ns_steps": self.steps,
@@ -592,9 +602,9 @@ class HipMuon:
         pos = {pid: k for k, pid in enumerate(ids)}
         with torch.no_grad():
             for p in self.model_params:
-                self.momentum[p].zero_()
+                self._momentum(p).zero_()
             for pid, st in state_dict["state"].items():
-                self.momentum[self.model_params[pos[pid]]].copy_(st["momentum_buffer"])
+                self._momentum(self.model_params[pos[pid]]).copy_(st["momentum_buffer"])
         if hyper:
             lr, wd, beta, nesterov, coeffs, eps, steps, adjust = hyper.pop()
             adjust = "original" if adjust is None else adjust

@@ -25,7 +25,7 @@ import torch
 import torch.nn as nn
 
 from .adamw.hip_adam import HipAdamW
-from .muon.hip_muon import HipMuon
+from .muon.hip_muon import _ADJUST_FNS, HipMuon
 
 ParameterGroups: TypeAlias = dict[str, list[nn.Parameter]]
 
@@ -217,7 +217,10 @@ class MuonAdamW(HipMuon, HipAdamW, torch.optim.Optimizer):
         a.lr, (a.beta1, a.beta2), a.eps, a.weight_decay = ga["lr"], ga["betas"], ga["eps"], ga["weight_decay"]
         m.lr, m.beta, m.is_nesterov, m.eps = gm["lr"], gm["momentum"], gm["nesterov"], gm["eps"]
         (m.a, m.b, m.c), m.steps, m.weight_decay = gm["ns_coefficients"], gm["ns_steps"], gm["weight_decay"]
-        m.adjust_lr_fn = gm["adjust_lr_fn"]
+        adjust = "original" if gm["adjust_lr_fn"] is None else gm["adjust_lr_fn"]  # torch's None
+        if adjust not in _ADJUST_FNS:
+            raise AssertionError(f"Invalid adjust_lr_fn: {adjust}")
+        m.adjust_lr_fn = adjust
 
     def _push_groups(self) -> None:
         """The branches' hyperparameters (after a load) into ``param_groups``."""
