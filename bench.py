@@ -276,7 +276,7 @@ def c1_layout():
 
 
 def bench_c1(dev, seed: int):
-    """Config 1 (the toy MLP of BASELINE config 1) on the GPU: one MuonAdamW step, ms (event loop of
+    """Config 1 (the toy MLP of BASELINE.json config 1) on the GPU: one MuonAdamW step, ms (event loop of
     20 steps after 5 warm-up)."""
     import torch
 
@@ -557,19 +557,19 @@ def bench_vs_torch_gpu(dev, seed: int = 0):
       build's MuonAdamW against PyTorchMuonAdamW, eager and, as the reference
       times it, compiled by torch.compile (inductor); warm-up 50, 100 timed
       steps, mean of 5 loops (:99-126).  Published: 1.24-1.26x against the
-      compiled step (README.md:48).
+      compiled step (the reference's README.md:48).
     * ref_muon_mlp: the reference's Muon benchmark model (five bias-free
       linear layers, muon_benchmark.py:14-24, all to Muon), HipMuon against
       torch.optim.Muon with the reference's settings (:33-35), eager and
       compiled; warm-up 50, 100 timed steps, mean of 5 loops (:66-92).
-      Published: 1.33-1.35x eager, 1.27-1.30x compiled (README.md:46-47).
+      Published: 1.33-1.35x eager, 1.27-1.30x compiled (the reference's README.md:46-47).
     * ref_adamw_mlp: the reference's AdamW benchmark model
       (adam_benchmark.py:14-25,33-42), HipAdamW against fused torch AdamW
       and against torch's default (foreach) AdamW; warm-up 100, 500 timed
       steps, mean of 10 loops (:75-108).  Published: 0.97-0.99x against the
-      fused and 2.65-2.70x against the foreach step (README.md:44-45).
+      fused and 2.65-2.70x against the foreach step (the reference's README.md:44-45).
     * gpt2, llama_layer (layer 0 plus 1/32 of the embedding and LM head),
-      c2_adamw: the BASELINE configurations, shorter loops.
+      c2_adamw: configurations 4, 5 and 2, shorter loops.
     """
     import torch
     import torch.nn as nn
@@ -671,7 +671,7 @@ def bench_vs_torch_gpu(dev, seed: int = 0):
     out["ref_adamw_mlp"] = r
     log(f"[vs torch gpu] reference AdamW MLP: {r}")
     del mine, ref, ref_fe, a, b, pa, pb
-    # BASELINE configurations
+    # BASELINE.json configurations
     mc, ac = configs()
     for name, layout in (("gpt2", gpt2_layout()),
                          ("llama_layer", [(n, s, br) for n, s, br in llama8b_layout() if n.startswith("l0.")]
