@@ -239,6 +239,17 @@ def test_muon_step_rejects_before_hip():
     arr = _mats([(256, 512), (512, 256)])
     arr[1].param = arr[0].param  # two entries update the same parameter
     assert _step(arr, 2) == ALIAS
+    # across entries, whatever one entry writes must stay clear of what another reads or writes
+    for field_i, field_j in (("momentum", "grad"), ("param", "momentum"), ("grad", "param"), ("update", "param"),
+                             ("momentum", "update")):
+        arr = _mats([(256, 512), (512, 256), (256, 512)])
+        for a in arr:
+            a.update = a.param + (3 << 34)
+        setattr(arr[2], field_i, getattr(arr[1], field_j) + 64)
+        assert _step(arr, 3) == ALIAS, (field_i, field_j)
+    arr = _mats([(256, 512), (512, 256), (300, 512)])
+    arr[1].grad = arr[0].grad  # two entries reading one gradient is fine: entries 0 and 1 pass,
+    assert _step(arr, 3) == SHAPE  # and validation stops at entry 2's shape
     arr = _mats([(256, 512)])
     arr[0].grad = arr[0].param + 4
     assert _step(arr, 1) == ALIAS

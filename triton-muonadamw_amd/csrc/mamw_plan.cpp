@@ -196,11 +196,22 @@ int muon_validate(const mamw_muon_matrix* mats, int batch, int ns_steps, const v
                 overlap(M.update, nb, M.momentum, nb) || overlap(M.update, nb, workspace, plan->bytes))
                 return MAMW_ERR_ALIAS;
         }
-        for (int j = 0; j < i; ++j) {  // two entries updating the same memory race
-            const size_t nej = size_t(mats[j].rows) * size_t(mats[j].cols);
-            const size_t npj = nej * ((mats[j].flags & MAMW_BF16_PARAM) ? 2 : 4);
-            if (overlap(M.param, np_, mats[j].param, npj) || overlap(M.momentum, nb, mats[j].momentum, nej * 4))
-                return MAMW_ERR_ALIAS;
+        // Across entries: memory one entry writes (parameter, momentum,
+        // update) must not overlap anything another entry reads or writes
+        // (the batch's kernels run over all entries at once).
+        const void* wi[3] = {M.param, M.momentum, M.update};
+        const size_t wbi[3] = {np_, nb, M.update ? nb : 0};
+        for (int j = 0; j < i; ++j) {
+            const mamw_muon_matrix& N = mats[j];
+            const size_t nej = size_t(N.rows) * size_t(N.cols);
+            const void* wj[3] = {N.param, N.momentum, N.update};
+            const size_t wbj[3] = {nej * ((N.flags & MAMW_BF16_PARAM) ? 2 : 4), nej * 4, N.update ? nej * 4 : 0};
+            const size_t ngj = nej * ((N.flags & MAMW_BF16_GRAD) ? 2 : 4);
+            for (int x = 0; x < 3; ++x) {
+                if (overlap(wi[x], wbi[x], N.grad, ngj) || overlap(wj[x], wbj[x], M.grad, ng)) return MAMW_ERR_ALIAS;
+                for (int y = 0; y < 3; ++y)
+                    if (overlap(wi[x], wbi[x], wj[y], wbj[y])) return MAMW_ERR_ALIAS;
+            }
         }
         MuonMatDesc& d = descs->d[i];
         d.param = M.param;
