@@ -110,6 +110,10 @@ int mamw_adamw_tensor_step(float* param, const float* grad, float* exp_avg,
  *    64-byte record per tensor plus one that mamw_adamw_mt_step_amp writes).
  * 2. mamw_adamw_table_pack (host only, no HIP call): validates the tensors and
  *    packs the table into host memory; returns the launch's block count.
+ *    Memory one tensor writes (param, exp_avg, exp_avg_sq) overlapping memory
+ *    any tensor of the table reads or writes is MAMW_ERR_ALIAS (the launch
+ *    updates them all at once), a parameter listed twice included: split such
+ *    a list over several tables, one launch each, for updates in sequence.
  * 3. The caller copies the table to device memory (16-byte aligned) and keeps
  *    it there while the pointers stay the same.
  * 4. mamw_adamw_mt_step: launches the update over every packed tensor.        */

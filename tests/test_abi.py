@@ -137,6 +137,35 @@ def test_adamw_pack_rejects(bad, code):
     assert st == code
 
 
+def test_adamw_pack_rejects_aliasing_across_tensors():
+    """One launch updates every tensor of a table at once: what a tensor writes
+    must stay clear of what any other tensor reads or writes (a parameter
+    listed twice included); gradients may be shared.  Both packers."""
+    BP = _lib.BF16_PARAM
+    a = _t(1 << 40, 1000)  # 4000-byte buffers
+    assert _pack([a, _t(2 << 40, 1000)])[0] == OK
+    a_bufs = [a.param, a.grad, a.exp_avg, a.exp_avg_sq]
+    for j, d in ((0, 0), (1, 8), (2, 4000 - 16), (3, 64)):  # somewhere in each of a's buffers
+        for k in (0, 2, 3):  # one of the second tensor's written buffers lands there
+            f = [(2 << 40) + i * (1 << 30) for i in range(4)]
+            f[k] = a_bufs[j] + d
+            assert _pack([a, _lib.AdamWTensor(*f, 1000)])[0] == ALIAS, (j, k)
+            assert _pack_ex([_lib.AdamWTensorEx(*f, 1000, 0, 0), _tx(1 << 40, 1000, 0)])[0] == ALIAS, (j, k)
+    b = _t(2 << 40, 1000)
+    b.grad = a.grad  # a shared gradient is only read
+    assert _pack([a, b])[0] == OK
+    b.grad = a.param + 3996  # reads the last element a writes
+    assert _pack([a, b])[0] == ALIAS
+    b.grad = a.param + 4000  # the next byte on: clear
+    assert _pack([a, b])[0] == OK
+    assert _pack([a, _t(1 << 40, 1000)])[0] == ALIAS  # the same tensor twice
+    # extents per element type: a bf16 parameter of 1000 elements ends 2000 bytes on
+    other = [(2 << 40) + i * (1 << 30) for i in range(4)]
+    for grad, code in (((1 << 40) + 2000, OK), ((1 << 40) + 1996, ALIAS)):
+        e = _lib.AdamWTensorEx(other[0], grad, other[2], other[3], 1000, 0, 0)
+        assert _pack_ex([_tx(1 << 40, 1000, BP), e])[0] == code
+
+
 def test_adamw_pack_small_table_and_counts():
     lib = _lib.load()
     arr = (_lib.AdamWTensor * 2)(_t(1 << 40, 10), _t(2 << 40, 10))

@@ -96,6 +96,43 @@ def test_adamw_skips_none_grad_but_counts_step(gpu):
     assert opt.step_num == 2
 
 
+def test_adamw_parameter_listed_twice_updates_in_sequence(gpu):
+    """A parameter listed k times is updated k times in sequence, each with the
+    step's one bias correction, as the reference's per-parameter loop does
+    (triton_adam.py:137-153; its state is keyed by the parameter): launch pass
+    i takes every parameter's i-th occurrence.  Bit-exact against the oracle's
+    update applied that many times, for a plain step and for a gradient-scaler
+    step (its device counter advances once per step, not once per pass; a
+    skipped step leaves everything and the counter as they were)."""
+    ps, gs, ms, vs = _params([1000, 4097, 333], gpu, seed=9)
+    a, b, c = (torch.nn.Parameter(p.to(gpu)) for p in ps)
+    opt = HipAdamW([a, b, a, c, a], **HP)
+    times = {0: 3, 1: 1, 2: 1}
+    ref = [[p.numpy().copy(), np.zeros_like(p.numpy()), np.zeros_like(p.numpy())] for p in ps]
+    for step in (1, 2, 3):
+        for p, g in zip((a, b, c), gs):
+            p.grad = (g * 4.0).to(gpu) if step > 1 else g.to(gpu)
+        if step == 1:
+            opt.step()
+        else:
+            found = torch.tensor(1.0 if step == 3 else 0.0, device=gpu)
+            opt._step_amp(torch.tensor(4.0, device=gpu), found)
+        if step == 3:
+            continue
+        b1, b2 = oracle.adamw.bias_corrections(0.9, 0.95, step)
+        for i, r in enumerate(ref):
+            for _ in range(times[i]):
+                r[:] = oracle.adamw.adamw_update(*r[:1], gs[i].numpy(), *r[1:], lr=HP["lr"], bias1=b1, bias2=b2,
+                                                 beta1=0.9, beta2=0.95, weight_decay=HP["weight_decay"],
+                                                 eps=HP["eps"])
+    torch.cuda.synchronize()
+    assert opt.step_num == 2
+    for p, r in zip((a, b, c), ref):
+        assert np.array_equal(p.detach().cpu().numpy(), r[0])
+        assert np.array_equal(opt.m[p].cpu().numpy(), r[1])
+        assert np.array_equal(opt.v[p].cpu().numpy(), r[2])
+
+
 def test_solve_adamw_step_bitexact(gpu):
     ps, gs, ms, vs = _params([4097 * 3], gpu, seed=5)
     p, g, m, v = (t[0].to(gpu) for t in (ps, gs, ms, vs))

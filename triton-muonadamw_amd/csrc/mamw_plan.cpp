@@ -3,6 +3,9 @@
 
 #include <string.h>
 
+#include <algorithm>
+#include <vector>
+
 namespace mamw {
 
 namespace {
@@ -10,6 +13,40 @@ namespace {
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 bool overlap(const void* a, size_t na, const void* b, size_t nb) { return ranges_overlap(a, na, b, nb); }
+
+// Across the tensors of one table (one launch runs them all at once): memory
+// a tensor writes (param, exp_avg, exp_avg_sq) must not overlap memory any
+// tensor reads or writes; gradients may be shared.  One sort of the byte
+// ranges and a sweep, so large tables stay cheap.
+struct Span {
+    uintptr_t lo, hi;
+    bool write;
+};
+
+int adamw_cross_alias(const mamw_adamw_tensor_ex* t, int n) {
+    if (n < 2) return MAMW_OK;
+    std::vector<Span> s;
+    s.reserve(size_t(n) * 4);
+    for (int i = 0; i < n; ++i) {
+        if (t[i].numel <= 0) continue;
+        const size_t ne = size_t(t[i].numel);
+        const size_t ep = (t[i].flags & MAMW_BF16_PARAM) ? 2 : 4, eg = (t[i].flags & MAMW_BF16_GRAD) ? 2 : 4;
+        const void* ptr[4] = {t[i].param, t[i].exp_avg, t[i].exp_avg_sq, t[i].grad};
+        const size_t len[4] = {ne * ep, ne * 4, ne * 4, ne * eg};
+        for (int k = 0; k < 4; ++k) {
+            const uintptr_t lo = reinterpret_cast<uintptr_t>(ptr[k]);
+            s.push_back({lo, lo + len[k], k < 3});
+        }
+    }
+    std::sort(s.begin(), s.end(), [](const Span& x, const Span& y) { return x.lo < y.lo; });
+    uintptr_t end_any = 0, end_write = 0;  // furthest end of the ranges before, of any kind / written
+    for (const Span& x : s) {
+        if (x.lo < (x.write ? end_any : end_write)) return MAMW_ERR_ALIAS;
+        end_any = std::max(end_any, x.hi);
+        if (x.write) end_write = std::max(end_write, x.hi);
+    }
+    return MAMW_OK;
+}
 
 }  // namespace
 
@@ -78,6 +115,8 @@ int adamw_table_pack_ex(const mamw_adamw_tensor_ex* tensors, int n_tensors, void
         blocks += (t.numel + kAdamWChunk - 1) / kAdamWChunk;
         if (blocks > int64_t(0x7fffffff)) return MAMW_ERR_NUMEL;  // grid.x limit
     }
+    const int st = adamw_cross_alias(tensors, n_tensors);
+    if (st != MAMW_OK) return st;
     if (n_tensors > 0) memset(&rec[n_tensors], 0, sizeof(AdamWRec));  // written by the device-counter step
     *n_blocks = blocks;
     return MAMW_OK;
@@ -89,7 +128,8 @@ int adamw_table_pack(const mamw_adamw_tensor* tensors, int n_tensors, void* host
     if (n_tensors < 0 || n_tensors > kMaxTensors) return MAMW_ERR_COUNT;
     if (n_tensors > 0 && (!tensors || !host_table)) return MAMW_ERR_NULL;
     if (n_tensors > 0 && table_bytes < size_t(n_tensors + 1) * sizeof(AdamWRec)) return MAMW_ERR_TABLE;
-    // fp32 entries are packed one at a time through the general path (no allocation).
+    // fp32 entries are packed one at a time through the general path; the
+    // cross-tensor check then sees them together (one host array).
     AdamWRec* rec = static_cast<AdamWRec*>(host_table);
     int64_t blocks = 0;
     for (int i = 0; i < n_tensors; ++i) {
@@ -101,6 +141,15 @@ int adamw_table_pack(const mamw_adamw_tensor* tensors, int n_tensors, void* host
         rec[i].block_begin = blocks;
         blocks += nb;
         if (blocks > int64_t(0x7fffffff)) return MAMW_ERR_NUMEL;
+    }
+    if (n_tensors > 1) {
+        std::vector<mamw_adamw_tensor_ex> ex(static_cast<size_t>(n_tensors));
+        for (int i = 0; i < n_tensors; ++i) {
+            const mamw_adamw_tensor& t = tensors[i];
+            ex[size_t(i)] = mamw_adamw_tensor_ex{t.param, t.grad, t.exp_avg, t.exp_avg_sq, t.numel, 0, 0};
+        }
+        const int st = adamw_cross_alias(ex.data(), n_tensors);
+        if (st != MAMW_OK) return st;
     }
     *n_blocks = blocks;
     return MAMW_OK;

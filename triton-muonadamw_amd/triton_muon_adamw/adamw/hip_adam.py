@@ -142,7 +142,12 @@ class HipAdamW:
         return m, self.v[param]
 
     def _build_plans(self, active: list[nn.Parameter]) -> None:
-        by_dev: dict[torch.device, list] = {}
+        # A parameter listed k times is updated k times in sequence, as the
+        # reference's per-parameter loop does (triton_adam.py:138-153): its
+        # i-th occurrence goes to launch pass i (one table per pass and
+        # device; a table may hold a tensor only once).
+        passes: list[dict[torch.device, list]] = []
+        seen: dict[int, int] = {}
         for p in active:
             g = p.grad
             _check_tensor(p, "param", bf16_ok=True)
@@ -152,8 +157,11 @@ class HipAdamW:
             m, v = self._moments(p)
             _check_tensor(m, "exp_avg")
             _check_tensor(v, "exp_avg_sq")
-            by_dev.setdefault(p.device, []).append((p, g, m, v))
-        self._plans = [_DevicePlan(dev, ents) for dev, ents in by_dev.items()]
+            k = seen[id(p)] = seen.get(id(p), -1) + 1
+            if k == len(passes):
+                passes.append({})
+            passes[k].setdefault(p.device, []).append((p, g, m, v))
+        self._plans = [_DevicePlan(dev, ents) for by_dev in passes for dev, ents in by_dev.items()]
 
     @property
     def step_num(self) -> int:
@@ -235,22 +243,31 @@ class HipAdamW:
             start = float(self._step_host)
             self._dev_steps = {plan.device: torch.full((), start, dtype=torch.float32, device=plan.device)
                                for plan in self._plans}
-        for plan in self._plans:
-            dev = plan.device
+        # Per device: the counter advances once, every pass of the step reads
+        # it, and a skipped step takes it back once.
+        amp: dict = {}
+        for dev in dict.fromkeys(plan.device for plan in self._plans):
             if dev not in self._dev_steps:
                 self._dev_steps[dev] = next(iter(self._dev_steps.values())).to(dev)
-            counter = self._dev_steps[dev]
             gs = grad_scale.to(dev, torch.float32, non_blocking=True) if grad_scale is not None else None
             fi = found_inf.to(dev, torch.float32, non_blocking=True) if found_inf is not None else None
+            amp[dev] = (gs, fi)
             with torch.cuda.device(dev):
-                counter.add_(1.0)
+                self._dev_steps[dev].add_(1.0)
+        for plan in self._plans:
+            dev = plan.device
+            gs, fi = amp[dev]
+            with torch.cuda.device(dev):
                 st = lib.mamw_adamw_mt_step_amp(
                     plan.table.data_ptr(), plan.n_tensors, plan.n_blocks, self.lr, self.beta1, self.beta2,
-                    self.weight_decay, self.eps, counter.data_ptr(), gs.data_ptr() if gs is not None else None,
-                    fi.data_ptr() if fi is not None else None, plan.launch_stream())
-                _lib.check(st, "mamw_adamw_mt_step_amp")
-                if fi is not None:
-                    counter.sub_(fi)
+                    self.weight_decay, self.eps, self._dev_steps[dev].data_ptr(),
+                    gs.data_ptr() if gs is not None else None, fi.data_ptr() if fi is not None else None,
+                    plan.launch_stream())
+            _lib.check(st, "mamw_adamw_mt_step_amp")
+        for dev, (_, fi) in amp.items():
+            if fi is not None:
+                with torch.cuda.device(dev):
+                    self._dev_steps[dev].sub_(fi)
 
     def zero_grad(self, set_to_none: bool = False):
         """Resets gradients back to zero (the reference's behaviour), or to None
