@@ -171,6 +171,32 @@ def test_batched_equals_single(gpu):
         assert torch.equal(a.detach(), b.detach())
 
 
+def test_parameter_listed_twice_steps_twice(gpu):
+    """A matrix listed twice gets two Muon updates in sequence (momentum and
+    parameter), as the reference's per-parameter loop gives it
+    (triton_muon.py:415-448, state keyed by the parameter): its second
+    occurrence goes to a later launch.  Equal bit for bit to the same matrix
+    stepped twice alone; the other member once."""
+    ps, gs, ms = muon_inputs([(256, 512), (512, 256)], seed=6)
+    w, u = (torch.nn.Parameter(p.to(gpu)) for p in ps)
+    opt = HipMuon([w, u, w], lr=2e-2, coeffs=COEFFS)
+    for p, g, m in zip((w, u), gs, ms):
+        p.grad = g.to(gpu)
+        opt.momentum[p].copy_(m)
+    opt.step()
+    assert [c.n for c in opt._calls] == [2, 1]
+    for p, p0, g, m, times in ((w, ps[0], gs[0], ms[0], 2), (u, ps[1], gs[1], ms[1], 1)):
+        q = torch.nn.Parameter(p0.to(gpu))
+        q.grad = g.to(gpu)
+        o = HipMuon([q], lr=2e-2, coeffs=COEFFS)
+        o.momentum[q].copy_(m)
+        for _ in range(times):
+            o.step()
+        torch.cuda.synchronize()
+        assert torch.equal(p.detach(), q.detach())
+        assert torch.equal(opt.momentum[p], o.momentum[q])
+
+
 def test_rect_tile_does_not_change_the_bits(gpu):
     """Twelve 768 x 3072 matrices (the tall and the wide orientation) in one
     launch group run their updates on 128 x 192 tiles (1152 tiles, at least
