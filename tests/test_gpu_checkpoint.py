@@ -377,6 +377,37 @@ def test_capture_refuses_a_plan_change(gpu):
     assert opt.adamw.step_num == 1
 
 
+def test_launch_plan_follows_the_parameters_layout(gpu):
+    """The cached launch plan is keyed by each parameter's and gradient's
+    address, type, shape and strides: a parameter whose ``.data`` becomes a
+    view starting at the same address (fewer rows, or every other row) is
+    checked again at the next step and rejected (its optimizer state no longer
+    matches; a strided view is not contiguous) before anything launches, with
+    the AdamW step counter unchanged.  Restoring the original tensor steps
+    again."""
+    p = torch.nn.Parameter(torch.randn(512, 256, device=gpu) * 0.02)
+    w = torch.nn.Parameter(torch.randn(512, 256, device=gpu) * 0.02)
+    opt = MuonAdamW({"adam": [p], "muon": [w]}, muon_config=MC, adam_config=AC, parameter_split="explicit")
+    full_p, full_w = p.data, w.data
+    for q in (p, w):
+        q.grad = torch.randn_like(q) * 1e-3
+    opt.step()
+    torch.cuda.synchronize()
+    for view, err in ((lambda t: t[:256], "shape"), (lambda t: t[::2], "contiguous")):
+        for q, full in ((p, full_p), (w, full_w)):
+            q.data = view(full)
+            q.grad = torch.randn_like(q) * 1e-3
+            assert q.data_ptr() == full.data_ptr()
+            with pytest.raises(ValueError, match=err):
+                opt.step()
+            assert opt.adamw.step_num == 1
+            q.data = full
+            q.grad = torch.randn_like(q) * 1e-3
+    opt.step()
+    torch.cuda.synchronize()
+    assert opt.adamw.step_num == 2
+
+
 def test_load_state_dict_keeps_the_captured_step_counter(gpu):
     """``capturable=True``: loading a checkpoint after a step was captured
     writes the loaded step into the device counter the graph advances (the

@@ -182,6 +182,15 @@ def require_gpu_tensor(t: torch.Tensor, name: str) -> None:
             "(there is no CPU path)")
 
 
+def layout_key(p: torch.Tensor) -> tuple:
+    """What a cached launch plan assumes of a parameter and its gradient:
+    addresses, element types and layouts.  A step whose parameters differ in
+    any of these builds a new plan (e.g. ``p.data`` replaced by a view that
+    starts at the same address with another shape)."""
+    g = p.grad
+    return (id(p), p.data_ptr(), p.dtype, p.shape, p.stride(), g.data_ptr(), g.dtype, g.shape, g.stride())
+
+
 def check_not_capturing(branch: str) -> None:
     """Launch plans and device step counters are made by eager steps only: a
     graph replays the pointers, scalars and table upload recorded at capture."""

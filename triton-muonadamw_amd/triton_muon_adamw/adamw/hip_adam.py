@@ -157,6 +157,9 @@ class HipAdamW:
             m, v = self._moments(p)
             _check_tensor(m, "exp_avg")
             _check_tensor(v, "exp_avg_sq")
+            if m.shape != p.shape or v.shape != p.shape:
+                raise ValueError(f"moments of shape {tuple(m.shape)} / {tuple(v.shape)} for a parameter of "
+                                 f"shape {tuple(p.shape)}")
             k = seen[id(p)] = seen.get(id(p), -1) + 1
             if k == len(passes):
                 passes.append({})
@@ -188,35 +191,26 @@ class HipAdamW:
             self._dev_steps: dict[torch.device, torch.Tensor] = {}
 
     def _refresh_plans(self, active: list[nn.Parameter]) -> None:
-        key = tuple((id(p), p.data_ptr(), p.grad.data_ptr(), p.dtype, p.grad.dtype) for p in active)
+        key = tuple(_lib.layout_key(p) for p in active)
         if key != self._plan_key:
             _lib.check_not_capturing("AdamW")
             self._plan_key = None
             self._build_plans(active)
             self._plan_key = key
 
+    def _plan(self) -> list[nn.Parameter]:
+        """The parameters that have a gradient, with their launch plan checked
+        (rebuilt when any of them changed): argument errors raise here, before
+        anything of the step is queued or counted."""
+        active = [p for p in self.model_params if p.grad is not None]
+        if active:
+            self._refresh_plans(active)
+        return active
+
     @torch.no_grad()
     def step(self):
         """Performs one iteration of the AdamW optimizer step."""
-        if self.capturable or self._dev_steps:
-            # The counter lives on the device (capturable, or after a gradient-
-            # scaler step): keep it there, so that no step reads it back.
-            self._step_amp(None, None)
-            return
-        self.step_num += 1
-        active = [p for p in self.model_params if p.grad is not None]
-        if not active:
-            return
-        self._refresh_plans(active)
-        lib = _lib.load()
-        bias1 = 1 - self.beta1**self._step_host
-        bias2 = 1 - self.beta2**self._step_host
-        for plan in self._plans:
-            with torch.cuda.device(plan.device):
-                st = lib.mamw_adamw_mt_step(
-                    plan.table.data_ptr(), plan.n_tensors, plan.n_blocks, self.lr, bias1, bias2,
-                    self.beta1, self.beta2, self.weight_decay, self.eps, plan.launch_stream())
-            _lib.check(st, "mamw_adamw_mt_step")
+        self._launch(self._plan(), None, None)
 
     @torch.no_grad()
     def _step_amp(self, grad_scale: torch.Tensor | None, found_inf: torch.Tensor | None) -> None:
@@ -226,7 +220,29 @@ class HipAdamW:
         non-zero, and the step counter incremented before the launch and
         decremented by ``found_inf`` after it, on the device.  Gradients are
         read, not rewritten."""
-        active = [p for p in self.model_params if p.grad is not None]
+        self._launch(self._plan(), grad_scale, found_inf, amp=True)
+
+    def _launch(self, active: list[nn.Parameter], grad_scale: torch.Tensor | None,
+                found_inf: torch.Tensor | None, amp: bool = False) -> None:
+        """Queue the step over ``active`` (planned by :meth:`_plan`)."""
+        if not amp and (self.capturable or self._dev_steps):
+            # The counter lives on the device (capturable, or after a gradient-
+            # scaler step): keep it there, so that no step reads it back.
+            amp = True
+        if not amp:
+            self.step_num += 1
+            if not active:
+                return
+            lib = _lib.load()
+            bias1 = 1 - self.beta1**self._step_host
+            bias2 = 1 - self.beta2**self._step_host
+            for plan in self._plans:
+                with torch.cuda.device(plan.device):
+                    st = lib.mamw_adamw_mt_step(
+                        plan.table.data_ptr(), plan.n_tensors, plan.n_blocks, self.lr, bias1, bias2,
+                        self.beta1, self.beta2, self.weight_decay, self.eps, plan.launch_stream())
+                _lib.check(st, "mamw_adamw_mt_step")
+            return
         if not active:  # nothing to update: the counter alone
             if self._dev_steps:
                 for c in self._dev_steps.values():
@@ -236,7 +252,6 @@ class HipAdamW:
             elif found_inf is None or float(found_inf) == 0.0:
                 self._step_host += 1
             return
-        self._refresh_plans(active)
         lib = _lib.load()
         if not self._dev_steps:
             _lib.check_not_capturing("AdamW")
@@ -245,18 +260,18 @@ class HipAdamW:
                                for plan in self._plans}
         # Per device: the counter advances once, every pass of the step reads
         # it, and a skipped step takes it back once.
-        amp: dict = {}
+        scaler: dict = {}
         for dev in dict.fromkeys(plan.device for plan in self._plans):
             if dev not in self._dev_steps:
                 self._dev_steps[dev] = next(iter(self._dev_steps.values())).to(dev)
             gs = grad_scale.to(dev, torch.float32, non_blocking=True) if grad_scale is not None else None
             fi = found_inf.to(dev, torch.float32, non_blocking=True) if found_inf is not None else None
-            amp[dev] = (gs, fi)
+            scaler[dev] = (gs, fi)
             with torch.cuda.device(dev):
                 self._dev_steps[dev].add_(1.0)
         for plan in self._plans:
             dev = plan.device
-            gs, fi = amp[dev]
+            gs, fi = scaler[dev]
             with torch.cuda.device(dev):
                 st = lib.mamw_adamw_mt_step_amp(
                     plan.table.data_ptr(), plan.n_tensors, plan.n_blocks, self.lr, self.beta1, self.beta2,
@@ -264,7 +279,7 @@ class HipAdamW:
                     gs.data_ptr() if gs is not None else None, fi.data_ptr() if fi is not None else None,
                     plan.launch_stream())
             _lib.check(st, "mamw_adamw_mt_step_amp")
-        for dev, (_, fi) in amp.items():
+        for dev, (_, fi) in scaler.items():
             if fi is not None:
                 with torch.cuda.device(dev):
                     self._dev_steps[dev].sub_(fi)

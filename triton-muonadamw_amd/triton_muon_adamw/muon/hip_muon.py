@@ -420,6 +420,9 @@ class HipMuon:
             if g.shape != p.shape or g.device != p.device:
                 raise ValueError("param.grad must match the parameter's shape and device")
             _check_matrix(self._momentum(p), "momentum")
+            if self.momentum[p].shape != p.shape:
+                raise ValueError(f"momentum buffer of shape {tuple(self.momentum[p].shape)} for a parameter of "
+                                 f"shape {tuple(p.shape)}")
             R, C = p.shape
             groups.setdefault((p.device, min(R, C), max(R, C)), []).append(p)
         calls = []
@@ -474,7 +477,7 @@ class HipMuon:
     @torch.no_grad()
     def step(self):
         """Optimizer step for the Muon optimizer."""
-        self._run(None, None)
+        self._run(self._plan(), None, None)
 
     @torch.no_grad()
     def _step_amp(self, grad_scale: torch.Tensor | None, found_inf: torch.Tensor | None) -> None:
@@ -482,14 +485,16 @@ class HipMuon:
         device: gradients divided by ``grad_scale``; where ``found_inf`` is
         non-zero the momentum and the parameters are left untouched (no host
         synchronisation).  Gradients are read, not rewritten."""
-        self._run(grad_scale, found_inf)
+        self._run(self._plan(), grad_scale, found_inf)
 
-    def _run(self, grad_scale: torch.Tensor | None, found_inf: torch.Tensor | None) -> None:
+    def _plan(self) -> list[nn.Parameter]:
+        """The parameters that have a gradient, with the launch plan checked
+        (rebuilt when any of them changed): argument errors raise here, before
+        anything of the step is queued."""
         active = [p for p in self.model_params if p.grad is not None]
         if not active:
-            return
-        key = (self.adjust_lr_fn, self.steps,
-               tuple((id(p), p.data_ptr(), p.grad.data_ptr(), p.dtype, p.grad.dtype) for p in active))
+            return active
+        key = (self.adjust_lr_fn, self.steps, tuple(_lib.layout_key(p) for p in active))
         if key != self._plan_key:
             _lib.check_not_capturing("Muon")
             self._plan_key = None
@@ -502,6 +507,13 @@ class HipMuon:
                     e = call.arr[i]
                     e.scaled_lr = scaled_lr(self.lr, self.adjust_lr_fn, e.rows, e.cols)
             self._plan_lr = self.lr
+        return active
+
+    def _run(self, active: list[nn.Parameter], grad_scale: torch.Tensor | None,
+             found_inf: torch.Tensor | None) -> None:
+        """Queue the step over ``active`` (planned by :meth:`_plan`)."""
+        if not active:
+            return
         lib = _lib.load()
         nest = int(bool(self.is_nesterov))
 

@@ -249,12 +249,13 @@ class MuonAdamW(HipMuon, HipAdamW, torch.optim.Optimizer):
         self._pull_groups()
         grad_scale = getattr(self, "grad_scale", None)
         found_inf = getattr(self, "found_inf", None)
-        if grad_scale is None and found_inf is None:
-            self.adamw.step()
-            self.muon.step()
-        else:
-            self.adamw._step_amp(grad_scale, found_inf)
-            self.muon._step_amp(grad_scale, found_inf)
+        amp = grad_scale is not None or found_inf is not None
+        with torch.no_grad():
+            # Both branches' plans first: an invalid argument in either raises
+            # before anything of the step is queued.
+            adam_active, muon_active = self.adamw._plan(), self.muon._plan()
+            self.adamw._launch(adam_active, grad_scale, found_inf, amp=amp)
+            self.muon._run(muon_active, grad_scale, found_inf)
         return loss
 
     def zero_grad(self, set_to_none: bool = False) -> None:
