@@ -115,6 +115,20 @@ def test_muonadamw_attributes_and_state_dict():
         assert opt.muon.momentum[p].shape == p.shape
 
 
+def test_parameters_join_a_branch_through_its_list():
+    """add_param_group is refused after construction (the two groups are the two
+    branches); a parameter appended to a branch's list joins that branch, with
+    zero state from its first use, and the torch.optim groups see it."""
+    opt = MuonAdamW(TinyLM())
+    with pytest.raises(ValueError, match="two fixed parameter groups"):
+        opt.add_param_group({"params": [nn.Parameter(torch.zeros(3))]})
+    extra = nn.Parameter(torch.zeros(4, 6))
+    opt.param_group["muon"].append(extra)
+    assert opt.param_groups[1]["params"][-1] is extra
+    mom = opt.state_dict()["muon"]["state"][len(opt.muon.model_params) - 1]["momentum_buffer"]
+    assert mom.shape == (4, 6) and not mom.any()
+
+
 def test_invalid_adjust_lr_fn_raises_assertion():
     with pytest.raises(AssertionError, match="Invalid adjust_lr_fn"):
         MuonAdamW(TinyLM(), MuonConfig(adjust_lr_fn="bogus"))

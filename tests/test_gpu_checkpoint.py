@@ -408,6 +408,47 @@ def test_launch_plan_follows_the_parameters_layout(gpu):
     assert opt.adamw.step_num == 2
 
 
+def test_parameter_appended_to_a_branch_steps_from_zero_state(gpu):
+    """A parameter appended to a branch's list after some steps takes part from
+    the next step on, from zero state: the Muon matrix equals a fresh
+    single-matrix optimizer's first step bit for bit; the AdamW vector gets
+    the global step counter's bias corrections (step 2, triton_adam.py:137),
+    bit-exact against the oracle from zero moments."""
+    import numpy as np
+
+    import oracle
+    from triton_muon_adamw.muon import HipMuon
+
+    p = torch.nn.Parameter(torch.randn(300, device=gpu) * 0.02)
+    w = torch.nn.Parameter(torch.randn(256, 512, device=gpu) * 0.02)
+    opt = MuonAdamW({"adam": [p], "muon": [w]}, muon_config=MC, adam_config=AC, parameter_split="explicit")
+    p.grad, w.grad = torch.randn_like(p) * 1e-3, torch.randn_like(w) * 1e-3
+    opt.step()
+    q = torch.nn.Parameter(torch.randn(1000, device=gpu) * 0.02)
+    u = torch.nn.Parameter(torch.randn(512, 384, device=gpu) * 0.02)
+    q0, u0 = q.detach().clone(), u.detach().clone()
+    opt.param_group["adam"].append(q)
+    opt.param_group["muon"].append(u)
+    for t in (p, w, q, u):
+        t.grad = torch.randn_like(t) * 1e-3
+    opt.step()
+    torch.cuda.synchronize()
+    v = torch.nn.Parameter(u0.clone())
+    v.grad = u.grad.clone()
+    twin = HipMuon([v], lr=MC.lr, weight_decay=MC.weight_decay, coeffs=MC.coeffs, nesterov=MC.nesterov,
+                   beta=MC.beta, ns_steps=MC.ns_steps, eps=MC.eps)
+    twin.step()
+    torch.cuda.synchronize()
+    assert torch.equal(u.detach(), v.detach())
+    b1, b2 = oracle.adamw.bias_corrections(AC.betas[0], AC.betas[1], 2)
+    zero = np.zeros(1000, np.float32)
+    exp = oracle.adamw.adamw_update(q0.cpu().numpy(), q.grad.cpu().numpy(), zero, zero, lr=AC.lr, bias1=b1,
+                                    bias2=b2, beta1=AC.betas[0], beta2=AC.betas[1],
+                                    weight_decay=AC.weight_decay, eps=AC.eps)
+    assert np.array_equal(q.detach().cpu().numpy(), exp[0])
+    assert opt.adamw.step_num == 2
+
+
 def test_load_state_dict_keeps_the_captured_step_counter(gpu):
     """``capturable=True``: loading a checkpoint after a step was captured
     writes the loaded step into the device counter the graph advances (the

@@ -197,8 +197,18 @@ class MuonAdamW(HipMuon, HipAdamW, torch.optim.Optimizer):
         }
         torch.optim.Optimizer.__init__(self, [self._adam_group(), self._muon_group()], {})
         self._push_groups()  # the groups share the branches' parameter lists
+        self._groups_fixed = True
 
     # -- torch.optim surface ---------------------------------------------------
+    def add_param_group(self, param_group: dict) -> None:
+        """Only at construction: the two groups ("adam", "muon") are the two
+        branches.  Later, a parameter joins a branch through its list
+        (``param_group["adam"]`` / ``["muon"]``, as in the reference)."""
+        if getattr(self, "_groups_fixed", False):
+            raise ValueError("MuonAdamW has two fixed parameter groups ('adam' and 'muon'); append parameters to "
+                             "param_group['adam'] or param_group['muon'] instead of add_param_group")
+        super().add_param_group(param_group)
+
     def _adam_group(self) -> dict:
         a = self.adamw
         return {"params": a.model_params, "lr": a.lr, "betas": (a.beta1, a.beta2), "eps": a.eps,
