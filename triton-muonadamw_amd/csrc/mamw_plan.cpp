@@ -26,7 +26,11 @@ struct Span {
 int adamw_cross_alias(const mamw_adamw_tensor_ex* t, int n) {
     if (n < 2) return MAMW_OK;
     std::vector<Span> s;
-    s.reserve(size_t(n) * 4);
+    try {  // no C++ exception may cross the C ABI
+        s.reserve(size_t(n) * 4);
+    } catch (...) {
+        return MAMW_ERR_COUNT;
+    }
     for (int i = 0; i < n; ++i) {
         if (t[i].numel <= 0) continue;
         const size_t ne = size_t(t[i].numel);
@@ -143,7 +147,12 @@ int adamw_table_pack(const mamw_adamw_tensor* tensors, int n_tensors, void* host
         if (blocks > int64_t(0x7fffffff)) return MAMW_ERR_NUMEL;
     }
     if (n_tensors > 1) {
-        std::vector<mamw_adamw_tensor_ex> ex(static_cast<size_t>(n_tensors));
+        std::vector<mamw_adamw_tensor_ex> ex;
+        try {  // no C++ exception may cross the C ABI
+            ex.resize(static_cast<size_t>(n_tensors));
+        } catch (...) {
+            return MAMW_ERR_COUNT;
+        }
         for (int i = 0; i < n_tensors; ++i) {
             const mamw_adamw_tensor& t = tensors[i];
             ex[size_t(i)] = mamw_adamw_tensor_ex{t.param, t.grad, t.exp_avg, t.exp_avg_sq, t.numel, 0, 0};

@@ -32,10 +32,20 @@ hipEvent_t take_event() {
     return e;
 }
 
+// Host allocations here may fail: no C++ exception may cross the C ABI, so a
+// record or an event that cannot be kept is dropped (an event is destroyed).
+void keep_free(hipEvent_t e) {
+    try {
+        g_free.push_back(e);
+    } catch (...) {
+        (void)hipEventDestroy(e);
+    }
+}
+
 void recycle_records() {
     for (Rec& r : g_recs) {
-        g_free.push_back(r.start);
-        g_free.push_back(r.stop);
+        keep_free(r.start);
+        keep_free(r.stop);
     }
     g_recs.clear();
 }
@@ -59,8 +69,8 @@ bool prof_take(hipEvent_t* start, hipEvent_t* stop) {
     *start = take_event();
     *stop = take_event();
     if (!*start || !*stop) {
-        if (*start) g_free.push_back(*start);
-        if (*stop) g_free.push_back(*stop);
+        if (*start) keep_free(*start);
+        if (*stop) keep_free(*stop);
         return false;
     }
     return true;
@@ -68,7 +78,12 @@ bool prof_take(hipEvent_t* start, hipEvent_t* stop) {
 
 void prof_push(int32_t kernel, int32_t variant, double flops, double bytes, hipEvent_t start, hipEvent_t stop) {
     std::lock_guard<std::mutex> lk(g_mu);
-    g_recs.push_back(Rec{kernel, variant, flops, bytes, start, stop});
+    try {
+        g_recs.push_back(Rec{kernel, variant, flops, bytes, start, stop});
+    } catch (...) {
+        keep_free(start);
+        keep_free(stop);
+    }
 }
 
 }  // namespace mamw
